@@ -1,0 +1,152 @@
+/*
+ * Model, run state and decode-step API of the MI355X build. C ABI.
+ *
+ * The types and functions replace William-Lamer/llm-inference src/model.cuh:10-64 and
+ * src/forward.cuh:6-34 with the same field names, argument order and fail-fast error
+ * behaviour (print to stderr, exit(EXIT_FAILURE); see llm_set_exit_on_error in kernels.h).
+ * The reference's 4096-position cap on the KV cache (src/forward.cu:7-8) is lifted: the cache
+ * holds max_seq_len positions, or the count given to alloc_run_state_seq.
+ */
+#ifndef LLM_AMD_FORWARD_H
+#define LLM_AMD_FORWARD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#include "kernels.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MAX_SHARDS 8
+#define MAX_EOS 8
+
+/* src/model.cuh:10-24 */
+typedef struct {
+    int hidden_size;
+    int intermediate_size;
+    int n_layers;
+    int n_heads;
+    int n_kv_heads;
+    int head_dim;
+    int vocab_size;
+    int max_seq_len;
+    float rms_norm_eps;
+    float rope_theta;
+    int tie_word_embeddings;
+    int eos_ids[MAX_EOS];
+    int n_eos;
+} Config;
+
+/* src/model.cuh:27-39. Matrices are PyTorch linear weights: [out, in], row-major. */
+typedef struct {
+    const bf16 *attn_norm;
+    const bf16 *wq;
+    const bf16 *wk;
+    const bf16 *wv;
+    const bf16 *q_norm;
+    const bf16 *k_norm;
+    const bf16 *wo;
+    const bf16 *mlp_norm;
+    const bf16 *w_gate;
+    const bf16 *w_up;
+    const bf16 *w_down;
+} LayerWeights;
+
+/* src/model.cuh:41-45 */
+typedef struct {
+    char name[96];
+    const bf16 *data;
+    size_t numel;
+} TensorRef;
+
+/* src/model.cuh:48-59. Host structs; the bf16 pointers point to device memory. */
+typedef struct {
+    const bf16 *embed;
+    LayerWeights *layers;
+    const bf16 *final_norm;
+    const bf16 *lm_head;
+
+    TensorRef *tensors;
+    int n_tensors;
+    void *gpu_buffers[MAX_SHARDS];
+    int n_buffers;
+    size_t gpu_bytes;
+} Weights;
+
+/* src/forward.cuh:6-25, plus the device state this build's step keeps after the reference's
+ * fields (attention workspace, argmax partials, the on-device token stream). */
+typedef struct {
+    bf16 *x;
+    bf16 *xb;
+    bf16 *q;
+    bf16 *k;
+    bf16 *v;
+    bf16 *attn_out;
+    float *att;            /* attention_workspace_floats(n_heads, head_dim, max_seq) */
+    bf16 *key_cache;       /* [n_layers, max_seq, n_kv_heads * head_dim] */
+    bf16 *value_cache;     /* [n_layers, max_seq, n_kv_heads * head_dim] */
+    int max_seq;
+    bf16 *hb;
+    bf16 *tap1;
+    bf16 *tap2;
+    bf16 *logits;
+    int *next_token;
+    int *pos;
+    hipStream_t stream;
+    hipGraphExec_t graph;
+    /* additions */
+    void *argmax_partials;  /* per-workgroup (value, index) pairs of the two-stage argmax */
+    int *token_out;         /* [token_capacity] tokens written by the on-device decode loop */
+    int token_capacity;
+    int *pos_base;          /* position of token_out[0] */
+    int *error_flag;        /* set on the device when a fed-back token is outside the vocab */
+    hipGraphExec_t loop_graph; /* step + argmax + token feedback + pos advance */
+} RunState;
+
+/* src/loader.cu:105-139 (config.json, generation_config.json) */
+void load_config(const char *model_dir, Config *cfg);
+/* src/loader.cu:313-380 (safetensors shards; BF16 only; 16-byte-aligned offsets) */
+void load_weights(const char *model_dir, const Config *cfg, Weights *w);
+void free_weights(Weights *w);
+/* src/loader.cu:395-419: "<name> <numel> <sum of bits> <index-weighted sum> <first value>" */
+void print_weight_checksums(const Weights *w);
+
+/* src/forward.cuh:27-34 */
+void alloc_run_state(RunState *s, const Config *cfg);
+void free_run_state(RunState *s);
+void capture_graph(const Config *cfg, const Weights *w, RunState *s);
+void forward(const Config *cfg, const Weights *w, RunState *s, int token, int pos);
+int sample_argmax(const Config *cfg, RunState *s);
+size_t weight_bytes_per_step(const Config *cfg);
+size_t kv_bytes_per_position(const Config *cfg);
+
+/* ---- additions ---- */
+
+/* alloc_run_state with a KV cache of max_seq positions (no cap). */
+void alloc_run_state_seq(RunState *s, const Config *cfg, int max_seq);
+
+/* Seeded random weights in the layout load_weights produces: every matrix and the embedding
+ * N(0, std), norm gammas 1 + N(0, gamma_std), lm_head tied to the embedding. One device buffer.
+ * Deterministic in (cfg shapes, seed). */
+void synth_weights(const Config *cfg, Weights *w, uint64_t seed, float std, float gamma_std);
+
+/* Fills n bf16 values at dev with mean + std * N(0,1) from the counter-based generator used by
+ * synth_weights (stream selects an independent sequence). */
+void synth_fill(bf16 *dev, size_t n, uint64_t seed, uint64_t stream_id, float mean, float std,
+                hipStream_t stream);
+
+/* Greedy decode entirely on the device: starting from `token` at position `pos`, replays the
+ * captured step n_steps times, feeding each argmax back as the next token. The n_steps greedy
+ * tokens are copied to out_tokens (host). One host synchronisation at the end. Returns 0, or
+ * -1 if a token left the vocabulary. */
+int generate_greedy(const Config *cfg, const Weights *w, RunState *s, int token, int pos,
+                    int n_steps, int *out_tokens);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,105 @@
+/*
+ * Decode-kernel launchers of the MI355X (gfx950) build. C ABI: plain device pointers, sizes and
+ * a hipStream_t; bf16 tensors are raw 16-bit patterns (uint16_t). Every pointer is caller-owned
+ * device memory and no launcher allocates. Launchers check shapes on the host; on a violation
+ * they print to stderr and exit(EXIT_FAILURE) like the reference, unless the error mode was
+ * switched with llm_set_exit_on_error(0), in which case they return without launching and
+ * llm_last_error() holds the message.
+ *
+ * Each entry point replaces the reference launcher of the same name in
+ * William-Lamer/llm-inference src/kernels.cuh (line numbers cited per function), with the same
+ * argument order and meaning.
+ */
+#ifndef LLM_AMD_KERNELS_H
+#define LLM_AMD_KERNELS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint16_t bf16;
+
+/* src/kernels.cuh:7-8. out[i] = table[*d_token * hidden + i]; the token is read on the device. */
+void embedding_forward(bf16 *out, const bf16 *table, const int *d_token, int hidden,
+                       hipStream_t stream);
+
+/* src/kernels.cuh:9-10. Per row: y = bf16(bf16(x * 1/sqrt(mean(x^2) + eps)) * weight). */
+void rmsnorm_forward(bf16 *out, const bf16 *in, const bf16 *weight, int rows, int dim, float eps,
+                     hipStream_t stream);
+
+/* src/kernels.cuh:11. out[r] = bf16(sum_c w[r, c] * x[c]), fp32 accumulation; cols % 8 == 0. */
+void gemv_forward(bf16 *out, const bf16 *w, const bf16 *x, int rows, int cols,
+                  hipStream_t stream);
+
+/* src/kernels.cuh:12-13. y = bf16(w[r] . in); tap[r] = y if tap != NULL; x[r] = bf16(x[r] + y).
+ * `in` must not alias `x`. cols % 8 == 0. */
+void gemv_residual_forward(bf16 *x, const bf16 *w, const bf16 *in, int rows, int cols, bf16 *tap,
+                           hipStream_t stream);
+
+/* src/kernels.cuh:14-15. q = wq.x, k = wk.x, v = wv.x in one launch. cols % 8 == 0. */
+void qkv_forward(bf16 *q, bf16 *k, bf16 *v, const bf16 *wq, const bf16 *wk, const bf16 *wv,
+                 const bf16 *x, int q_rows, int kv_rows, int cols, hipStream_t stream);
+
+/* src/kernels.cuh:16-17. g = bf16(w_gate[r].x), u = bf16(w_up[r].x) (taps when non-NULL),
+ * act[r] = bf16(bf16(g / (1 + exp(-g))) * u). cols % 8 == 0. */
+void gate_up_forward(bf16 *act, const bf16 *w_gate, const bf16 *w_up, const bf16 *x, int rows,
+                     int cols, bf16 *gate_tap, bf16 *up_tap, hipStream_t stream);
+
+/* src/kernels.cuh:18-21. Per head: RMSNorm over head_dim with q_norm_w/k_norm_w (normed heads to
+ * q_tap/k_tap when non-NULL), then RoPE at position *d_pos with inv_freq_j = 1/theta^(2j/D), in
+ * place on q [n_heads*D] and k [n_kv_heads*D]; k' and v are written to key_cache/value_cache
+ * (one layer's caches, [max_seq, n_kv_heads*D]) at row *d_pos. head_dim in {64, 128, 256}. */
+void qk_norm_rope_forward(bf16 *q, bf16 *k, const bf16 *v, const bf16 *q_norm_w,
+                          const bf16 *k_norm_w, bf16 *key_cache, bf16 *value_cache,
+                          const int *d_pos, int n_heads, int n_kv_heads, int head_dim, float eps,
+                          float theta, bf16 *q_tap, bf16 *k_tap, hipStream_t stream);
+
+/* src/kernels.cuh:22-24. Decode attention of the query at position *d_pos over cache rows
+ * 0..*d_pos, GQA kv_head = h / (n_heads / n_kv_heads). scores bf16(bf16(q.k) * scale), softmax
+ * probabilities rounded to bf16, out = bf16(sum p v). `att` is fp32 scratch of at least
+ * attention_workspace_floats(n_heads, head_dim, max_seq) floats: the reference's
+ * [n_heads, max_seq] score rows followed by the split-softmax block statistics and partial
+ * outputs. head_dim in {64, 128, 256}; n_heads / n_kv_heads in {1, 2, 4, 8}. */
+void attention_forward(bf16 *out, const bf16 *q, const bf16 *key_cache, const bf16 *value_cache,
+                       float *att, int n_heads, int n_kv_heads, int head_dim, const int *d_pos,
+                       int max_seq, float scale, hipStream_t stream);
+
+/* src/kernels.cuh:25. *out = index of the largest x; ties keep the lowest index; NaN is never
+ * taken (all-NaN input gives INT_MAX). Calls on one device must not overlap: the partial
+ * results live in one library-owned device buffer. */
+void argmax_forward(int *out, const bf16 *x, int n, hipStream_t stream);
+
+/* ---- entry points with no counterpart in kernels.cuh (needed by the multi-row workloads) ---- */
+
+/* qk_norm_rope_forward over n_tokens rows: q [n_tokens, n_heads*D], k and v
+ * [n_tokens, n_kv_heads*D]; token t uses position d_positions[t] for RoPE and its cache row.
+ * Taps, when non-NULL, have the shapes of q and k. */
+void qk_norm_rope_rows(bf16 *q, bf16 *k, const bf16 *v, const bf16 *q_norm_w,
+                       const bf16 *k_norm_w, bf16 *key_cache, bf16 *value_cache,
+                       const int *d_positions, int n_tokens, int n_heads, int n_kv_heads,
+                       int head_dim, float eps, float theta, bf16 *q_tap, bf16 *k_tap,
+                       hipStream_t stream);
+
+/* act[i] = bf16(bf16(g / (1 + exp(-g))) * up[i]) with g = gate[i], the elementwise tail of
+ * gate_up_forward (src/kernels.cu:283-286). */
+void swiglu_forward(bf16 *act, const bf16 *gate, const bf16 *up, size_t n, hipStream_t stream);
+
+/* Floats attention_forward needs in `att` for these sizes. */
+size_t attention_workspace_floats(int n_heads, int head_dim, int max_seq);
+
+/* Error mode: 1 (default) = print and exit(EXIT_FAILURE) like the reference; 0 = record the
+ * message, skip the launch and return. Returns the previous mode. */
+int llm_set_exit_on_error(int enable);
+/* Message of the last recorded error of this thread, or NULL. */
+const char *llm_last_error(void);
+void llm_clear_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

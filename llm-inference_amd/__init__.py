@@ -1,0 +1,205 @@
+"""Python host side of the MI355X (gfx950) decode kernels.
+
+Thin ctypes bindings of libllm_amd.so, whose C ABI (include/llm_amd/kernels.h, forward.h)
+replaces the reference's src/kernels.cuh and src/forward.cuh launchers and step API
+(William-Lamer/llm-inference). The wrappers take torch tensors for device memory and a torch
+stream (or the current one); torch is only the allocator and stream provider. Every call goes to
+the HIP kernels: there is no CPU path, and a missing library raises.
+
+Errors the reference reports with exit(EXIT_FAILURE) raise LlmError here (the library is
+switched to recording mode on load).
+"""
+import ctypes
+import os
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "libllm_amd.so"
+
+__all__ = [
+    "LlmError", "lib", "embedding_forward", "rmsnorm_forward", "gemv_forward",
+    "gemv_residual_forward", "qkv_forward", "gate_up_forward", "qk_norm_rope_forward",
+    "qk_norm_rope_rows", "attention_forward", "argmax_forward", "swiglu_forward",
+    "attention_workspace_floats", "EXPORTED_SYMBOLS",
+]
+
+# Every symbol include/llm_amd/*.h declares.
+EXPORTED_SYMBOLS = [
+    "embedding_forward", "rmsnorm_forward", "gemv_forward", "gemv_residual_forward",
+    "qkv_forward", "gate_up_forward", "qk_norm_rope_forward", "attention_forward",
+    "argmax_forward", "qk_norm_rope_rows", "swiglu_forward", "attention_workspace_floats",
+    "llm_set_exit_on_error", "llm_last_error", "llm_clear_error",
+    "load_config", "load_weights", "free_weights", "print_weight_checksums",
+    "alloc_run_state", "free_run_state", "capture_graph", "forward", "sample_argmax",
+    "weight_bytes_per_step", "kv_bytes_per_position", "alloc_run_state_seq", "synth_weights",
+    "synth_fill", "generate_greedy",
+]
+
+
+class LlmError(RuntimeError):
+    """A shape, alignment or HIP error reported by libllm_amd."""
+
+
+_lib = None
+
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+_f = ctypes.c_float
+_sz = ctypes.c_size_t
+
+_SIGS = {
+    "embedding_forward": (None, [_vp, _vp, _vp, _i, _vp]),
+    "rmsnorm_forward": (None, [_vp, _vp, _vp, _i, _i, _f, _vp]),
+    "gemv_forward": (None, [_vp, _vp, _vp, _i, _i, _vp]),
+    "gemv_residual_forward": (None, [_vp, _vp, _vp, _i, _i, _vp, _vp]),
+    "qkv_forward": (None, [_vp] * 7 + [_i, _i, _i, _vp]),
+    "gate_up_forward": (None, [_vp] * 4 + [_i, _i, _vp, _vp, _vp]),
+    "qk_norm_rope_forward": (None, [_vp] * 8 + [_i, _i, _i, _f, _f, _vp, _vp, _vp]),
+    "qk_norm_rope_rows": (None, [_vp] * 8 + [_i, _i, _i, _i, _f, _f, _vp, _vp, _vp]),
+    "attention_forward": (None, [_vp] * 5 + [_i, _i, _i, _vp, _i, _f, _vp]),
+    "argmax_forward": (None, [_vp, _vp, _i, _vp]),
+    "swiglu_forward": (None, [_vp, _vp, _vp, _sz, _vp]),
+    "attention_workspace_floats": (_sz, [_i, _i, _i]),
+    "llm_set_exit_on_error": (_i, [_i]),
+    "llm_last_error": (ctypes.c_char_p, []),
+    "llm_clear_error": (None, []),
+}
+
+
+def lib():
+    """The loaded libllm_amd.so (raises LlmError if it has not been built)."""
+    global _lib
+    if _lib is None:
+        # torch first: its bundled HIP runtime then satisfies the library's libamdhip64.so.7
+        # dependency (same SONAME), so both share one runtime and torch's streams are valid here.
+        import torch  # noqa: F401
+        if not LIB_PATH.exists():
+            raise LlmError(f"{LIB_PATH} is missing: build it with `make -C {HERE}` "
+                           "(or __graft_entry__.build())")
+        L = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        L.llm_set_exit_on_error(0)
+        _lib = L
+        from . import model  # noqa: F401  (declares the step API signatures)
+        model._declare(L)
+    return _lib
+
+
+def check():
+    """Raises LlmError with the library's message if the last call recorded an error."""
+    L = lib()
+    msg = L.llm_last_error()
+    if msg is not None:
+        L.llm_clear_error()
+        raise LlmError(msg.decode())
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    if not t.is_cuda:
+        raise LlmError("tensors passed to the HIP kernels must live on the GPU")
+    if not t.is_contiguous():
+        raise LlmError("tensors passed to the HIP kernels must be contiguous")
+    return t.data_ptr()
+
+
+def _bf16(t, name):
+    import torch
+    if t is not None and not isinstance(t, int) and t.dtype not in (torch.bfloat16, torch.int16,
+                                                                     torch.uint16):
+        raise LlmError(f"{name} must be bfloat16 (or its raw 16-bit view), got {t.dtype}")
+    return _ptr(t)
+
+
+def _stream(stream):
+    import torch
+    if stream is None:
+        return torch.cuda.current_stream().cuda_stream
+    if isinstance(stream, int):
+        return stream
+    return stream.cuda_stream
+
+
+def _call(fn, *args):
+    fn(*args)
+    check()
+
+
+# ---- launchers (include/llm_amd/kernels.h) ----
+
+def embedding_forward(out, table, d_token, hidden, stream=None):
+    _call(lib().embedding_forward, _bf16(out, "out"), _bf16(table, "table"), _ptr(d_token),
+          hidden, _stream(stream))
+
+
+def rmsnorm_forward(out, inp, weight, rows, dim, eps, stream=None):
+    _call(lib().rmsnorm_forward, _bf16(out, "out"), _bf16(inp, "in"), _bf16(weight, "weight"),
+          rows, dim, eps, _stream(stream))
+
+
+def gemv_forward(out, w, x, rows, cols, stream=None):
+    _call(lib().gemv_forward, _bf16(out, "out"), _bf16(w, "w"), _bf16(x, "x"), rows, cols,
+          _stream(stream))
+
+
+def gemv_residual_forward(x, w, inp, rows, cols, tap=None, stream=None):
+    _call(lib().gemv_residual_forward, _bf16(x, "x"), _bf16(w, "w"), _bf16(inp, "in"), rows,
+          cols, _bf16(tap, "tap"), _stream(stream))
+
+
+def qkv_forward(q, k, v, wq, wk, wv, x, q_rows, kv_rows, cols, stream=None):
+    _call(lib().qkv_forward, _bf16(q, "q"), _bf16(k, "k"), _bf16(v, "v"), _bf16(wq, "wq"),
+          _bf16(wk, "wk"), _bf16(wv, "wv"), _bf16(x, "x"), q_rows, kv_rows, cols,
+          _stream(stream))
+
+
+def gate_up_forward(act, w_gate, w_up, x, rows, cols, gate_tap=None, up_tap=None, stream=None):
+    _call(lib().gate_up_forward, _bf16(act, "act"), _bf16(w_gate, "w_gate"), _bf16(w_up, "w_up"),
+          _bf16(x, "x"), rows, cols, _bf16(gate_tap, "gate_tap"), _bf16(up_tap, "up_tap"),
+          _stream(stream))
+
+
+def qk_norm_rope_forward(q, k, v, q_norm_w, k_norm_w, key_cache, value_cache, d_pos, n_heads,
+                         n_kv_heads, head_dim, eps, theta, q_tap=None, k_tap=None, stream=None):
+    _call(lib().qk_norm_rope_forward, _bf16(q, "q"), _bf16(k, "k"), _bf16(v, "v"),
+          _bf16(q_norm_w, "q_norm_w"), _bf16(k_norm_w, "k_norm_w"), _bf16(key_cache, "key_cache"),
+          _bf16(value_cache, "value_cache"), _ptr(d_pos), n_heads, n_kv_heads, head_dim, eps,
+          theta, _bf16(q_tap, "q_tap"), _bf16(k_tap, "k_tap"), _stream(stream))
+
+
+def qk_norm_rope_rows(q, k, v, q_norm_w, k_norm_w, key_cache, value_cache, d_positions,
+                      n_tokens, n_heads, n_kv_heads, head_dim, eps, theta, q_tap=None,
+                      k_tap=None, stream=None):
+    _call(lib().qk_norm_rope_rows, _bf16(q, "q"), _bf16(k, "k"), _bf16(v, "v"),
+          _bf16(q_norm_w, "q_norm_w"), _bf16(k_norm_w, "k_norm_w"), _bf16(key_cache, "key_cache"),
+          _bf16(value_cache, "value_cache"), _ptr(d_positions), n_tokens, n_heads, n_kv_heads,
+          head_dim, eps, theta, _bf16(q_tap, "q_tap"), _bf16(k_tap, "k_tap"), _stream(stream))
+
+
+def attention_workspace_floats(n_heads, head_dim, max_seq):
+    return lib().attention_workspace_floats(n_heads, head_dim, max_seq)
+
+
+def attention_forward(out, q, key_cache, value_cache, att, n_heads, n_kv_heads, head_dim, d_pos,
+                      max_seq, scale, stream=None):
+    need = attention_workspace_floats(n_heads, head_dim, max_seq)
+    if not isinstance(att, int) and att.numel() < need:
+        raise LlmError(f"att holds {att.numel()} floats, attention needs {need}")
+    _call(lib().attention_forward, _bf16(out, "out"), _bf16(q, "q"),
+          _bf16(key_cache, "key_cache"), _bf16(value_cache, "value_cache"), _ptr(att), n_heads,
+          n_kv_heads, head_dim, _ptr(d_pos), max_seq, scale, _stream(stream))
+
+
+def argmax_forward(out, x, n, stream=None):
+    _call(lib().argmax_forward, _ptr(out), _bf16(x, "x"), n, _stream(stream))
+
+
+def swiglu_forward(act, gate, up, n, stream=None):
+    _call(lib().swiglu_forward, _bf16(act, "act"), _bf16(gate, "gate"), _bf16(up, "up"), n,
+          _stream(stream))

@@ -1,0 +1,396 @@
+// Decode step of the gfx950 build: run state, the per-layer launch order of the reference's
+// forward_kernels (src/forward.cu:118-193) on this build's kernels, hipGraph capture and replay,
+// greedy sampling, and a decode loop that stays on the device (argmax feeds the next step's
+// embedding, the position advances in a kernel, tokens are copied out once at the end).
+#include <math.h>
+#include <string.h>
+
+#include "common.h"
+#include "internal.h"
+#include "llm_amd/forward.h"
+
+using namespace llm;
+
+// ------------------------------------------------------------------------------------------
+// run state (src/forward.cu:10-73)
+// ------------------------------------------------------------------------------------------
+
+static bool dmalloc(void **p, size_t bytes) {
+    *p = nullptr;
+    if (!HIP_OK(hipMalloc(p, bytes))) return false;
+    return HIP_OK(hipMemset(*p, 0, bytes));
+}
+
+extern "C" void alloc_run_state_seq(RunState *s, const Config *cfg, int max_seq) {
+    memset(s, 0, sizeof *s);
+    if (max_seq <= 0) {
+        llm_fail("alloc_run_state: max_seq %d must be positive", max_seq);
+        return;
+    }
+    const size_t q_dim = (size_t)cfg->n_heads * cfg->head_dim;
+    const size_t kv_dim = (size_t)cfg->n_kv_heads * cfg->head_dim;
+    const size_t H = cfg->hidden_size, I = cfg->intermediate_size;
+    s->max_seq = max_seq;
+    const size_t cache_len = (size_t)cfg->n_layers * max_seq * kv_dim;
+    size_t tap_len = q_dim;
+    if (I > tap_len) tap_len = I;
+    if (H > tap_len) tap_len = H;
+    const size_t att = attention_workspace_floats(cfg->n_heads, cfg->head_dim, max_seq);
+    bool ok = dmalloc((void **)&s->x, H * 2) && dmalloc((void **)&s->xb, H * 2) &&
+              dmalloc((void **)&s->q, q_dim * 2) && dmalloc((void **)&s->k, kv_dim * 2) &&
+              dmalloc((void **)&s->v, kv_dim * 2) && dmalloc((void **)&s->attn_out, q_dim * 2) &&
+              dmalloc((void **)&s->att, att * 4) && dmalloc((void **)&s->key_cache, cache_len * 2) &&
+              dmalloc((void **)&s->value_cache, cache_len * 2) && dmalloc((void **)&s->hb, I * 2) &&
+              dmalloc((void **)&s->tap1, tap_len * 2) && dmalloc((void **)&s->tap2, tap_len * 2) &&
+              dmalloc((void **)&s->logits, (size_t)cfg->vocab_size * 2) &&
+              dmalloc((void **)&s->next_token, 4) && dmalloc((void **)&s->pos, 4) &&
+              dmalloc(&s->argmax_partials, (size_t)argmax_partial_count() * 8) &&
+              dmalloc((void **)&s->pos_base, 4) && dmalloc((void **)&s->error_flag, 4);
+    if (!ok) return;
+    HIP_OK(hipStreamCreate(&s->stream));
+}
+
+extern "C" void alloc_run_state(RunState *s, const Config *cfg) {
+    alloc_run_state_seq(s, cfg, cfg->max_seq_len);
+}
+
+extern "C" void free_run_state(RunState *s) {
+    void *bufs[] = {s->x,  s->xb,     s->q,      s->k,      s->v,          s->attn_out,
+                    s->att, s->key_cache, s->value_cache, s->hb, s->tap1, s->tap2,
+                    s->logits, s->next_token, s->pos, s->argmax_partials, s->token_out,
+                    s->pos_base, s->error_flag};
+    for (void *b : bufs)
+        if (b) HIP_OK(hipFree(b));
+    if (s->graph) HIP_OK(hipGraphExecDestroy(s->graph));
+    if (s->loop_graph) HIP_OK(hipGraphExecDestroy(s->loop_graph));
+    if (s->stream) HIP_OK(hipStreamDestroy(s->stream));
+    memset(s, 0, sizeof *s);
+}
+
+// ------------------------------------------------------------------------------------------
+// byte counts (src/forward.cu:83-114)
+// ------------------------------------------------------------------------------------------
+
+extern "C" size_t weight_bytes_per_step(const Config *cfg) {
+    const size_t H = cfg->hidden_size, D = cfg->head_dim;
+    const size_t q_dim = (size_t)cfg->n_heads * D, kv_dim = (size_t)cfg->n_kv_heads * D;
+    const size_t I = cfg->intermediate_size;
+    // norms, q/k/v, q/k norms, o, mlp norm, gate/up/down
+    const size_t layer = H + q_dim * H + 2 * kv_dim * H + 2 * D + H * q_dim + H + 2 * I * H + H * I;
+    // layers, final norm, LM head, one embedding row
+    const size_t elements = layer * cfg->n_layers + H + (size_t)cfg->vocab_size * H + H;
+    return elements * 2;
+}
+
+extern "C" size_t kv_bytes_per_position(const Config *cfg) {
+    return 2 * (size_t)cfg->n_layers * cfg->n_kv_heads * cfg->head_dim * 2;
+}
+
+// ------------------------------------------------------------------------------------------
+// the step
+// ------------------------------------------------------------------------------------------
+
+static bool forward_kernels(const Config *cfg, const Weights *w, RunState *s) {
+    const int H = cfg->hidden_size, D = cfg->head_dim;
+    const int q_dim = cfg->n_heads * D, kv_dim = cfg->n_kv_heads * D;
+    const int I = cfg->intermediate_size;
+    const float scale = (float)(1.0 / sqrt((double)D));
+    hipStream_t st = s->stream;
+    embedding_checked(s->x, w->embed, s->next_token, H, cfg->vocab_size, s->error_flag, st);
+    for (int l = 0; l < cfg->n_layers && !llm_has_error(); l++) {
+        const LayerWeights *L = &w->layers[l];
+        bf16 *kc = s->key_cache + (size_t)l * s->max_seq * kv_dim;
+        bf16 *vc = s->value_cache + (size_t)l * s->max_seq * kv_dim;
+        rmsnorm_forward(s->xb, s->x, L->attn_norm, 1, H, cfg->rms_norm_eps, st);
+        qkv_forward(s->q, s->k, s->v, L->wq, L->wk, L->wv, s->xb, q_dim, kv_dim, H, st);
+        qk_norm_rope_forward(s->q, s->k, s->v, L->q_norm, L->k_norm, kc, vc, s->pos, cfg->n_heads,
+                             cfg->n_kv_heads, D, cfg->rms_norm_eps, cfg->rope_theta, nullptr,
+                             nullptr, st);
+        attention_forward(s->attn_out, s->q, kc, vc, s->att, cfg->n_heads, cfg->n_kv_heads, D,
+                          s->pos, s->max_seq, scale, st);
+        gemv_residual_forward(s->x, L->wo, s->attn_out, H, q_dim, nullptr, st);
+        rmsnorm_forward(s->xb, s->x, L->mlp_norm, 1, H, cfg->rms_norm_eps, st);
+        gate_up_forward(s->hb, L->w_gate, L->w_up, s->xb, I, H, nullptr, nullptr, st);
+        gemv_residual_forward(s->x, L->w_down, s->hb, H, I, nullptr, st);
+    }
+    rmsnorm_forward(s->xb, s->x, w->final_norm, 1, H, cfg->rms_norm_eps, st);
+    gemv_forward(s->logits, w->lm_head, s->xb, cfg->vocab_size, H, st);
+    return !llm_has_error();
+}
+
+static void argmax_into_next(const Config *cfg, RunState *s) {
+    float *pv = (float *)s->argmax_partials;
+    int *pi = (int *)(pv + argmax_partial_count());
+    argmax_launch(s->next_token, s->logits, cfg->vocab_size, pv, pi, s->stream);
+}
+
+// Token and position travel as kernel arguments, so no host buffer has to outlive the call.
+__global__ void set_token_pos_kernel(int *d_token, int *d_pos, int token, int pos) {
+    if (threadIdx.x == 0) {
+        *d_token = token;
+        *d_pos = pos;
+    }
+}
+
+// Records the next token and advances the position (the on-device decode loop).
+__global__ void advance_kernel(int *d_pos, const int *d_token, int *token_out,
+                               const int *pos_base, int capacity) {
+    if (threadIdx.x == 0) {
+        const int i = *d_pos - *pos_base;
+        if (i >= 0 && i < capacity) token_out[i] = *d_token;
+        *d_pos = *d_pos + 1;
+    }
+}
+
+static bool capture(hipStream_t st, hipGraphExec_t *exec, bool (*body)(void *), void *ctx) {
+    hipGraph_t graph;
+    if (!HIP_OK(hipStreamBeginCapture(st, hipStreamCaptureModeGlobal))) return false;
+    const bool ok = body(ctx);
+    hipError_t end = hipStreamEndCapture(st, &graph);
+    if (!ok) {
+        if (end == hipSuccess) (void)hipGraphDestroy(graph);
+        return false;
+    }
+    if (!HIP_OK(end)) return false;
+    const bool inst = HIP_OK(hipGraphInstantiate(exec, graph, nullptr, nullptr, 0));
+    HIP_OK(hipGraphDestroy(graph));
+    return inst;
+}
+
+struct StepCtx {
+    const Config *cfg;
+    const Weights *w;
+    RunState *s;
+};
+
+static bool step_body(void *p) {
+    StepCtx *c = (StepCtx *)p;
+    return forward_kernels(c->cfg, c->w, c->s);
+}
+
+static bool loop_body(void *p) {
+    StepCtx *c = (StepCtx *)p;
+    if (!forward_kernels(c->cfg, c->w, c->s)) return false;
+    argmax_into_next(c->cfg, c->s);
+    advance_kernel<<<1, 64, 0, c->s->stream>>>(c->s->pos, c->s->next_token, c->s->token_out,
+                                                c->s->pos_base, c->s->token_capacity);
+    return LAUNCH_OK();
+}
+
+// src/forward.cu:196-204
+extern "C" void capture_graph(const Config *cfg, const Weights *w, RunState *s) {
+    StepCtx c{cfg, w, s};
+    if (s->graph) {
+        HIP_OK(hipGraphExecDestroy(s->graph));
+        s->graph = nullptr;
+    }
+    capture(s->stream, &s->graph, step_body, &c);
+}
+
+static bool check_token_pos(const Config *cfg, const RunState *s, int token, int pos) {
+    if (token < 0 || token >= cfg->vocab_size)
+        return llm_fail("forward: token %d outside vocab of %d", token, cfg->vocab_size);
+    if (pos < 0 || pos >= s->max_seq)
+        return llm_fail("forward: position %d past the kv cache size %d", pos, s->max_seq);
+    return true;
+}
+
+// src/forward.cu:206-227
+extern "C" void forward(const Config *cfg, const Weights *w, RunState *s, int token, int pos) {
+    if (!check_token_pos(cfg, s, token, pos)) return;
+    set_token_pos_kernel<<<1, 64, 0, s->stream>>>(s->next_token, s->pos, token, pos);
+    if (!LAUNCH_OK()) return;
+    if (s->graph)
+        HIP_OK(hipGraphLaunch(s->graph, s->stream));
+    else
+        forward_kernels(cfg, w, s);
+}
+
+// src/forward.cu:229-236
+extern "C" int sample_argmax(const Config *cfg, RunState *s) {
+    argmax_into_next(cfg, s);
+    int token = -1;
+    if (!HIP_OK(hipMemcpyAsync(&token, s->next_token, 4, hipMemcpyDeviceToHost, s->stream)))
+        return -1;
+    if (!HIP_OK(hipStreamSynchronize(s->stream))) return -1;
+    return token;
+}
+
+extern "C" int generate_greedy(const Config *cfg, const Weights *w, RunState *s, int token,
+                               int pos, int n_steps, int *out_tokens) {
+    if (n_steps <= 0) return 0;
+    if (!check_token_pos(cfg, s, token, pos)) return -1;
+    if (pos + n_steps > s->max_seq) {
+        llm_fail("generate_greedy: %d steps from position %d pass the kv cache size %d", n_steps,
+                 pos, s->max_seq);
+        return -1;
+    }
+    if (s->token_capacity < n_steps || !s->loop_graph) {
+        if (s->token_capacity < n_steps) {
+            if (s->token_out) HIP_OK(hipFree(s->token_out));
+            int cap = n_steps < 256 ? 256 : n_steps;
+            if (!dmalloc((void **)&s->token_out, (size_t)cap * 4)) return -1;
+            s->token_capacity = cap;
+            if (s->loop_graph) {
+                HIP_OK(hipGraphExecDestroy(s->loop_graph));
+                s->loop_graph = nullptr;
+            }
+        }
+        StepCtx c{cfg, w, s};
+        if (!capture(s->stream, &s->loop_graph, loop_body, &c)) return -1;
+    }
+    set_token_pos_kernel<<<1, 64, 0, s->stream>>>(s->next_token, s->pos, token, pos);
+    set_token_pos_kernel<<<1, 64, 0, s->stream>>>(s->error_flag, s->pos_base, 0, pos);
+    if (!LAUNCH_OK()) return -1;
+    for (int i = 0; i < n_steps; i++)
+        if (!HIP_OK(hipGraphLaunch(s->loop_graph, s->stream))) return -1;
+    int err = 0;
+    if (!HIP_OK(hipMemcpyAsync(out_tokens, s->token_out, (size_t)n_steps * 4,
+                               hipMemcpyDeviceToHost, s->stream)) ||
+        !HIP_OK(hipMemcpyAsync(&err, s->error_flag, 4, hipMemcpyDeviceToHost, s->stream)) ||
+        !HIP_OK(hipStreamSynchronize(s->stream)))
+        return -1;
+    return err ? -1 : 0;
+}
+
+// ------------------------------------------------------------------------------------------
+// seeded synthetic weights
+// ------------------------------------------------------------------------------------------
+
+__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+    x += 0x9E3779B97F4A7C15ull;
+    x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+    x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+    return x ^ (x >> 31);
+}
+
+// Element pair (2i, 2i+1) of stream `sid` comes from two 53-bit uniforms of a counter-based
+// SplitMix64 sequence through the Box-Muller transform in double.
+__global__ __launch_bounds__(256) void synth_kernel(bf16 *out, size_t n, uint64_t seed,
+                                                    uint64_t sid, float mean, float std) {
+    const uint64_t key = splitmix64(seed ^ splitmix64(sid + 0x632BE59BD9B4E019ull));
+    const size_t pairs = (n + 1) / 2;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < pairs;
+         i += (size_t)gridDim.x * blockDim.x) {
+        const uint64_t a = splitmix64(key + 2 * i), b = splitmix64(key + 2 * i + 1);
+        const double u1 = (double)((a >> 11) + 1) * 0x1.0p-53;  // (0, 1]
+        const double u2 = (double)(b >> 11) * 0x1.0p-53;        // [0, 1)
+        const double r = sqrt(-2.0 * log(u1));
+        double sv, cv;
+        sincospi(2.0 * u2, &sv, &cv);
+        out[2 * i] = (bf16)f2bf((float)(mean + std * r * cv));
+        if (2 * i + 1 < n) out[2 * i + 1] = (bf16)f2bf((float)(mean + std * r * sv));
+    }
+}
+
+extern "C" void synth_fill(bf16 *dev, size_t n, uint64_t seed, uint64_t stream_id, float mean,
+                           float std, hipStream_t stream) {
+    if (n == 0) return;
+    size_t blocks = ((n + 1) / 2 + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    synth_kernel<<<(unsigned)blocks, 256, 0, stream>>>(dev, n, seed, stream_id, mean, std);
+    LAUNCH_OK();
+}
+
+struct SynthTensor {
+    char name[96];
+    size_t numel;
+    int norm;  // gamma: 1 + N(0, gamma_std)
+};
+
+static int synth_tensor_list(const Config *cfg, SynthTensor *list) {
+    const int H = cfg->hidden_size, D = cfg->head_dim, I = cfg->intermediate_size;
+    const size_t q_dim = (size_t)cfg->n_heads * D, kv_dim = (size_t)cfg->n_kv_heads * D;
+    int n = 0;
+    auto add = [&](const char *name, size_t numel, int norm) {
+        if (list) {
+            snprintf(list[n].name, sizeof list[n].name, "%s", name);
+            list[n].numel = numel;
+            list[n].norm = norm;
+        }
+        n++;
+    };
+    char name[96];
+    add("model.embed_tokens.weight", (size_t)cfg->vocab_size * H, 0);
+    for (int l = 0; l < cfg->n_layers; l++) {
+        const struct {
+            const char *suffix;
+            size_t numel;
+            int norm;
+        } parts[] = {{"input_layernorm.weight", (size_t)H, 1},
+                     {"self_attn.q_proj.weight", q_dim * H, 0},
+                     {"self_attn.k_proj.weight", kv_dim * H, 0},
+                     {"self_attn.v_proj.weight", kv_dim * H, 0},
+                     {"self_attn.q_norm.weight", (size_t)D, 1},
+                     {"self_attn.k_norm.weight", (size_t)D, 1},
+                     {"self_attn.o_proj.weight", (size_t)H * q_dim, 0},
+                     {"post_attention_layernorm.weight", (size_t)H, 1},
+                     {"mlp.gate_proj.weight", (size_t)I * H, 0},
+                     {"mlp.up_proj.weight", (size_t)I * H, 0},
+                     {"mlp.down_proj.weight", (size_t)H * I, 0}};
+        for (const auto &p : parts) {
+            snprintf(name, sizeof name, "model.layers.%d.%s", l, p.suffix);
+            add(name, p.numel, p.norm);
+        }
+    }
+    add("model.norm.weight", (size_t)H, 1);
+    return n;
+}
+
+extern "C" void synth_weights(const Config *cfg, Weights *w, uint64_t seed, float std,
+                              float gamma_std) {
+    memset(w, 0, sizeof *w);
+    const int n = synth_tensor_list(cfg, nullptr);
+    SynthTensor *list = (SynthTensor *)calloc(n, sizeof(SynthTensor));
+    w->tensors = (TensorRef *)calloc(n, sizeof(TensorRef));
+    w->layers = (LayerWeights *)calloc(cfg->n_layers, sizeof(LayerWeights));
+    if (!list || !w->tensors || !w->layers) {
+        free(list);
+        llm_fail("synth_weights: out of memory");
+        return;
+    }
+    synth_tensor_list(cfg, list);
+    // every tensor on a 256-byte boundary inside one allocation
+    size_t total = 0;
+    for (int i = 0; i < n; i++) total += (list[i].numel * 2 + 255) & ~(size_t)255;
+    char *base = nullptr;
+    if (!HIP_OK(hipMalloc((void **)&base, total))) {
+        free(list);
+        return;
+    }
+    size_t off = 0;
+    for (int i = 0; i < n; i++) {
+        bf16 *p = (bf16 *)(base + off);
+        off += (list[i].numel * 2 + 255) & ~(size_t)255;
+        synth_fill(p, list[i].numel, seed, (uint64_t)i, list[i].norm ? 1.0f : 0.0f,
+                   list[i].norm ? gamma_std : std, nullptr);
+        TensorRef *t = &w->tensors[i];
+        snprintf(t->name, sizeof t->name, "%s", list[i].name);
+        t->data = p;
+        t->numel = list[i].numel;
+    }
+    w->n_tensors = n;
+    w->embed = w->tensors[0].data;
+    for (int l = 0; l < cfg->n_layers; l++) {
+        const TensorRef *t = &w->tensors[1 + 11 * l];
+        LayerWeights *L = &w->layers[l];
+        L->attn_norm = t[0].data;
+        L->wq = t[1].data;
+        L->wk = t[2].data;
+        L->wv = t[3].data;
+        L->q_norm = t[4].data;
+        L->k_norm = t[5].data;
+        L->wo = t[6].data;
+        L->mlp_norm = t[7].data;
+        L->w_gate = t[8].data;
+        L->w_up = t[9].data;
+        L->w_down = t[10].data;
+    }
+    w->final_norm = w->tensors[n - 1].data;
+    w->lm_head = w->embed;
+    w->gpu_buffers[0] = base;
+    w->n_buffers = 1;
+    w->gpu_bytes = total;
+    free(list);
+    HIP_OK(hipDeviceSynchronize());
+}

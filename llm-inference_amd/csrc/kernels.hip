@@ -1,0 +1,1126 @@
+// Decode kernels for gfx950 (MI355X), behind the launcher names of the reference's
+// src/kernels.cuh. Wave64 throughout: a GEMV row is one wave whose lanes stream 16-byte chunks
+// (global_load_dwordx4, non-temporal for weights and the KV cache) and meet in an xor-butterfly
+// tree; RMSNorm rows up to 8192 wide are one wave held in registers; a RoPE head is a group of
+// D/16 lanes that each hold the chunk [8L, 8L+8) and its rotation partner [D/2+8L, ...), so the
+// rotation is lane-local. Arithmetic is fp32 with bf16 stores at the reference's rounding points
+// (src/kernels.cu), in the summation orders the CPU oracle restates.
+#include <limits.h>
+#include <math.h>
+#include <stdarg.h>
+#include <string.h>
+
+#include <mutex>
+
+#include "common.h"
+#include "internal.h"
+
+using namespace llm;
+
+// ------------------------------------------------------------------------------------------
+// error handling (src/common.cuh:11-22 semantics, switchable to recording)
+// ------------------------------------------------------------------------------------------
+
+static int g_exit_on_error = 1;
+static thread_local char g_err[1024];
+static thread_local bool g_has_err = false;
+
+bool llm_fail(const char *fmt, ...) {
+    char buf[1024];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    if (g_exit_on_error) {
+        fprintf(stderr, "%s\n", buf);
+        exit(EXIT_FAILURE);
+    }
+    if (!g_has_err) {  // keep the first error until it is cleared
+        strncpy(g_err, buf, sizeof g_err - 1);
+        g_err[sizeof g_err - 1] = 0;
+        g_has_err = true;
+    }
+    return false;
+}
+
+bool llm_has_error() { return g_has_err; }
+
+extern "C" int llm_set_exit_on_error(int enable) {
+    int old = g_exit_on_error;
+    g_exit_on_error = enable ? 1 : 0;
+    return old;
+}
+extern "C" const char *llm_last_error(void) { return g_has_err ? g_err : nullptr; }
+extern "C" void llm_clear_error(void) {
+    g_has_err = false;
+    g_err[0] = 0;
+}
+
+static bool aligned16(const void *p) { return ((uintptr_t)p & 15) == 0; }
+
+// ------------------------------------------------------------------------------------------
+// embedding (src/kernels.cu:7-23)
+// ------------------------------------------------------------------------------------------
+
+// One workgroup copies the row in 16-byte chunks. With vocab > 0 a token outside [0, vocab)
+// sets *err and copies nothing (the step uses this for tokens fed back on the device).
+__global__ __launch_bounds__(256) void embedding_kernel(bf16 *out, const bf16 *table,
+                                                        const int *d_token, int hidden, int vocab,
+                                                        int *err) {
+    const int token = *d_token;
+    if (vocab > 0 && (token < 0 || token >= vocab)) {
+        if (err && threadIdx.x == 0) *err = 1;
+        return;
+    }
+    const bf16 *row = table + (size_t)token * hidden;
+    if ((hidden & 7) == 0) {
+        for (int c = threadIdx.x; c < hidden / 8; c += blockDim.x) st16(out + 8 * c, ld16(row + 8 * c));
+    } else {
+        for (int i = threadIdx.x; i < hidden; i += blockDim.x) out[i] = row[i];
+    }
+}
+
+static void launch_embedding(bf16 *out, const bf16 *table, const int *d_token, int hidden,
+                             int vocab, int *err, hipStream_t stream) {
+    if (hidden <= 0) {
+        llm_fail("embedding: hidden %d must be positive", hidden);
+        return;
+    }
+    if ((hidden & 7) == 0 && (!aligned16(out) || !aligned16(table))) {
+        llm_fail("embedding: out and table must be 16-byte aligned");
+        return;
+    }
+    embedding_kernel<<<1, 256, 0, stream>>>(out, table, d_token, hidden, vocab, err);
+    LAUNCH_OK();
+}
+
+extern "C" void embedding_forward(bf16 *out, const bf16 *table, const int *d_token, int hidden,
+                                  hipStream_t stream) {
+    launch_embedding(out, table, d_token, hidden, 0, nullptr, stream);
+}
+
+// Used by the step for device-fed tokens.
+void embedding_checked(bf16 *out, const bf16 *table, const int *d_token, int hidden, int vocab,
+                       int *err, hipStream_t stream) {
+    launch_embedding(out, table, d_token, hidden, vocab, err, stream);
+}
+
+// ------------------------------------------------------------------------------------------
+// RMSNorm (src/kernels.cu:25-71)
+// ------------------------------------------------------------------------------------------
+
+// One wave per row, the row in registers: lane l holds chunks l, l+64, ... (NC of them).
+// sum of squares: per-lane fma in chunk/element order, then the wave tree.
+template <int NC>
+__global__ __launch_bounds__(256) void rmsnorm_wave_kernel(bf16 *out, const bf16 *in,
+                                                           const bf16 *weight, int rows, int dim,
+                                                           float eps) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int n_chunks = dim >> 3;
+    const bf16 *x = in + (size_t)row * dim;
+    u32x4 xv[NC], wv[NC];
+#pragma unroll
+    for (int k = 0; k < NC; k++) {
+        const int c = lane + 64 * k;
+        xv[k] = c < n_chunks ? ld16(x + 8 * c) : u32x4{0, 0, 0, 0};
+        wv[k] = c < n_chunks ? ld16(weight + 8 * c) : u32x4{0, 0, 0, 0};
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NC; k++) acc = dot8(xv[k], xv[k], acc);
+    const float total = wave_sum(acc);
+    const float inv = 1.0f / sqrtf(total / (float)dim + eps);
+    bf16 *y = out + (size_t)row * dim;
+#pragma unroll
+    for (int k = 0; k < NC; k++) {
+        const int c = lane + 64 * k;
+        if (c < n_chunks) {
+            float r[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) r[e] = round_bf(elem(xv[k], e) * inv) * elem(wv[k], e);
+            st16(y + 8 * c, u32x4{pack2(r[0], r[1]), pack2(r[2], r[3]), pack2(r[4], r[5]),
+                                  pack2(r[6], r[7])});
+        }
+    }
+}
+
+// Any dim: W waves per row (W = max(1, min(16, ceil(chunks / 1024)))), thread t takes chunks
+// t, t + 64W, ... element by element; wave trees, then the waves added in order through LDS.
+__global__ __launch_bounds__(1024) void rmsnorm_generic_kernel(bf16 *out, const bf16 *in,
+                                                               const bf16 *weight, int dim,
+                                                               float eps) {
+    __shared__ float part[16];
+    const int row = blockIdx.x;
+    const int T = blockDim.x;
+    const bf16 *x = in + (size_t)row * dim;
+    const int n_chunks = (dim + 7) / 8;
+    float acc = 0.0f;
+    for (int c = threadIdx.x; c < n_chunks; c += T)
+        for (int e = 0; e < 8; e++) {
+            const int i = 8 * c + e;
+            if (i < dim) {
+                const float v = bf2f(x[i]);
+                acc = fmaf(v, v, acc);
+            }
+        }
+    const float ws = wave_sum(acc);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ws;
+    __syncthreads();
+    float total = part[0];
+    for (int w = 1; w < T / 64; w++) total = total + part[w];
+    const float inv = 1.0f / sqrtf(total / (float)dim + eps);
+    bf16 *y = out + (size_t)row * dim;
+    for (int i = threadIdx.x; i < dim; i += T)
+        y[i] = f2bf(round_bf(bf2f(x[i]) * inv) * bf2f(weight[i]));
+}
+
+static int rms_waves(int dim) {
+    int n_chunks = (dim + 7) / 8;
+    int w = (n_chunks + 64 * 16 - 1) / (64 * 16);
+    return w < 1 ? 1 : (w > 16 ? 16 : w);
+}
+
+extern "C" void rmsnorm_forward(bf16 *out, const bf16 *in, const bf16 *weight, int rows, int dim,
+                                float eps, hipStream_t stream) {
+    if (rows <= 0 || dim <= 0) {
+        llm_fail("rmsnorm: rows %d and dim %d must be positive", rows, dim);
+        return;
+    }
+    const int per_lane = (dim / 8 + 63) / 64;
+    const bool fast = (dim & 7) == 0 && per_lane <= 16 && aligned16(out) && aligned16(in) &&
+                      aligned16(weight);
+    if (fast) {
+        const int blocks = (rows + 3) / 4;
+#define RMS(NC_)                                                                            \
+    if (per_lane <= NC_) {                                                                  \
+        rmsnorm_wave_kernel<NC_><<<blocks, 256, 0, stream>>>(out, in, weight, rows, dim, eps); \
+        LAUNCH_OK();                                                                        \
+        return;                                                                             \
+    }
+        RMS(1) RMS(2) RMS(3) RMS(4) RMS(5) RMS(6) RMS(8) RMS(12) RMS(16)
+#undef RMS
+    }
+    rmsnorm_generic_kernel<<<rows, 64 * rms_waves(dim), 0, stream>>>(out, in, weight, dim, eps);
+    LAUNCH_OK();
+}
+
+// ------------------------------------------------------------------------------------------
+// GEMV family (src/kernels.cu:79-212, :215-298)
+// ------------------------------------------------------------------------------------------
+
+// A launch covers up to three weight matrices against one input vector (qkv stacks
+// [wq; wk; wv]); each segment owns a contiguous range of waves.
+struct GemvSeg {
+    const bf16 *w;
+    bf16 *out;
+    int rows;
+    int wave_begin;
+};
+
+struct GemvArgs {
+    GemvSeg seg[3];
+    int n_seg;
+    const bf16 *x;
+    int cols;
+    bf16 *tap;  // residual epilogue: optional copy of y
+};
+
+enum { EPI_PLAIN = 0, EPI_RESID = 1 };
+
+// Wave `wave` computes RPW consecutive rows. Lane l streams chunks l, l+64, ... of each row
+// (NC per lane per panel, panels until the row ends), fma-accumulating in order; the wave tree
+// then gives every lane each row's sum and lane i stores row row0+i.
+template <int NC, int RPW, int EPI>
+__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int si = (a.n_seg > 2 && wave >= a.seg[2].wave_begin)   ? 2
+                   : (a.n_seg > 1 && wave >= a.seg[1].wave_begin) ? 1
+                                                                  : 0;
+    const bf16 *w = si == 0 ? a.seg[0].w : si == 1 ? a.seg[1].w : a.seg[2].w;
+    bf16 *out = si == 0 ? a.seg[0].out : si == 1 ? a.seg[1].out : a.seg[2].out;
+    const int rows = si == 0 ? a.seg[0].rows : si == 1 ? a.seg[1].rows : a.seg[2].rows;
+    const int wb = si == 0 ? a.seg[0].wave_begin : si == 1 ? a.seg[1].wave_begin : a.seg[2].wave_begin;
+    const int row0 = (wave - wb) * RPW;
+    if (row0 >= rows) return;
+    const int cols = a.cols;
+    const int n_chunks = cols >> 3;
+    float acc[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; i++) acc[i] = 0.0f;
+    for (int c0 = 0; c0 < n_chunks; c0 += 64 * NC) {
+        u32x4 xv[NC];
+        u32x4 wv[RPW][NC];
+#pragma unroll
+        for (int k = 0; k < NC; k++) {
+            const int c = c0 + lane + 64 * k;
+            xv[k] = c < n_chunks ? ld16(a.x + 8 * (size_t)c) : u32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int i = 0; i < RPW; i++) {
+            const int r = min(row0 + i, rows - 1);
+            const bf16 *wr = w + (size_t)r * cols;
+#pragma unroll
+            for (int k = 0; k < NC; k++) {
+                const int c = c0 + lane + 64 * k;
+                wv[i][k] = c < n_chunks ? ld16_nt(wr + 8 * (size_t)c) : u32x4{0, 0, 0, 0};
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < RPW; i++)
+#pragma unroll
+            for (int k = 0; k < NC; k++) acc[i] = dot8(wv[i][k], xv[k], acc[i]);
+    }
+    float mine = 0.0f;
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+        const float t = wave_sum(acc[i]);
+        if (lane == i) mine = t;
+    }
+    const int r = row0 + lane;
+    if (lane < RPW && r < rows) {
+        const uint32_t y = f2bf(mine);
+        if (EPI == EPI_PLAIN) {
+            out[r] = (bf16)y;
+        } else {
+            if (a.tap) a.tap[r] = (bf16)y;
+            out[r] = (bf16)f2bf(bf2f(out[r]) + bf2f((bf16)y));
+        }
+    }
+}
+
+// gate and up rows together: g = bf16(wg[r].x), u = bf16(wu[r].x),
+// act = bf16(bf16(silu(g)) * u) (src/kernels.cu:276-287).
+template <int NC, int RPW>
+__global__ __launch_bounds__(256) void gate_up_kernel(bf16 *act, const bf16 *wg, const bf16 *wu,
+                                                      const bf16 *x, int rows, int cols,
+                                                      bf16 *gate_tap, bf16 *up_tap) {
+    const int lane = threadIdx.x & 63;
+    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int row0 = wave * RPW;
+    if (row0 >= rows) return;
+    const int n_chunks = cols >> 3;
+    float ag[RPW], au[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; i++) ag[i] = au[i] = 0.0f;
+    for (int c0 = 0; c0 < n_chunks; c0 += 64 * NC) {
+        u32x4 xv[NC];
+        u32x4 gv[RPW][NC], uv[RPW][NC];
+#pragma unroll
+        for (int k = 0; k < NC; k++) {
+            const int c = c0 + lane + 64 * k;
+            xv[k] = c < n_chunks ? ld16(x + 8 * (size_t)c) : u32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int i = 0; i < RPW; i++) {
+            const size_t r = (size_t)min(row0 + i, rows - 1);
+#pragma unroll
+            for (int k = 0; k < NC; k++) {
+                const int c = c0 + lane + 64 * k;
+                const bool in = c < n_chunks;
+                gv[i][k] = in ? ld16_nt(wg + r * cols + 8 * (size_t)c) : u32x4{0, 0, 0, 0};
+                uv[i][k] = in ? ld16_nt(wu + r * cols + 8 * (size_t)c) : u32x4{0, 0, 0, 0};
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < RPW; i++)
+#pragma unroll
+            for (int k = 0; k < NC; k++) {
+                ag[i] = dot8(gv[i][k], xv[k], ag[i]);
+                au[i] = dot8(uv[i][k], xv[k], au[i]);
+            }
+    }
+    float g_mine = 0.0f, u_mine = 0.0f;
+#pragma unroll
+    for (int i = 0; i < RPW; i++) {
+        const float g = wave_sum(ag[i]);
+        const float u = wave_sum(au[i]);
+        if (lane == i) {
+            g_mine = g;
+            u_mine = u;
+        }
+    }
+    const int r = row0 + lane;
+    if (lane < RPW && r < rows) {
+        const bf16 g = (bf16)f2bf(g_mine);
+        const bf16 u = (bf16)f2bf(u_mine);
+        if (gate_tap) gate_tap[r] = g;
+        if (up_tap) up_tap[r] = u;
+        const float s = round_bf(silu_f32(bf2f(g)));
+        act[r] = (bf16)f2bf(s * bf2f(u));
+    }
+}
+
+// Per-lane chunk capacity of one panel.
+static int pick_nc(int n_chunks) {
+    const int per_lane = (n_chunks + 63) / 64;
+    static const int ncs[] = {1, 2, 3, 4, 5, 6, 8, 10, 12, 16, 20};
+    for (int v : ncs)
+        if (v >= per_lane) return v;
+    return 20;
+}
+
+// Rows per wave: enough loads in flight per lane (RPW*NC ~ 8-16) while keeping at least ~2048
+// waves (8 per CU) when the matrix has the rows for it.
+static int pick_rpw(int nc, long total_rows, int pairs) {
+    int rpw = nc <= 2 ? 8 : nc <= 4 ? 4 : nc <= 8 ? 2 : 1;
+    if (pairs) rpw = rpw > 1 ? rpw / 2 : 1;
+    while (rpw > 1 && total_rows / rpw < 2048) rpw /= 2;
+    return rpw;
+}
+
+static bool check_gemv(const char *name, const void *w, const void *x, int rows, int cols) {
+    if (cols % 8 != 0) return llm_fail("%s: cols %d is not a multiple of 8", name, cols);
+    if (rows <= 0 || cols <= 0) return llm_fail("%s: rows %d and cols %d must be positive", name, rows, cols);
+    if (!aligned16(w) || !aligned16(x))
+        return llm_fail("%s: weight and input must be 16-byte aligned", name);
+    return true;
+}
+
+#define GEMV_CASES(X) \
+    X(1, 1) X(1, 2) X(1, 4) X(1, 8) X(2, 1) X(2, 2) X(2, 4) X(2, 8) X(3, 1) X(3, 2) X(3, 4) \
+    X(4, 1) X(4, 2) X(4, 4) X(5, 1) X(5, 2) X(6, 1) X(6, 2) X(8, 1) X(8, 2) X(10, 1)    \
+    X(12, 1) X(16, 1) X(20, 1)
+
+template <int EPI>
+static bool dispatch_gemv(const GemvArgs &a, int nc, int rpw, int blocks, hipStream_t st) {
+#define X(NC_, RPW_)                                                         \
+    if (nc == NC_ && rpw == RPW_) {                                          \
+        gemv_kernel<NC_, RPW_, EPI><<<blocks, 256, 0, st>>>(a);              \
+        return LAUNCH_OK();                                                  \
+    }
+    GEMV_CASES(X)
+#undef X
+    return llm_fail("gemv: no kernel for nc %d rpw %d", nc, rpw);
+}
+
+static void launch_gemv(GemvArgs &a, int epi, hipStream_t stream) {
+    long total_rows = 0;
+    for (int i = 0; i < a.n_seg; i++) total_rows += a.seg[i].rows;
+    const int nc = pick_nc(a.cols / 8);
+    const int rpw = pick_rpw(nc, total_rows, 0);
+    int waves = 0;
+    for (int i = 0; i < a.n_seg; i++) {
+        a.seg[i].wave_begin = waves;
+        waves += (a.seg[i].rows + rpw - 1) / rpw;
+    }
+    const int blocks = (waves + 3) / 4;
+    if (epi == EPI_PLAIN)
+        dispatch_gemv<EPI_PLAIN>(a, nc, rpw, blocks, stream);
+    else
+        dispatch_gemv<EPI_RESID>(a, nc, rpw, blocks, stream);
+}
+
+extern "C" void gemv_forward(bf16 *out, const bf16 *w, const bf16 *x, int rows, int cols,
+                             hipStream_t stream) {
+    if (!check_gemv("gemv", w, x, rows, cols)) return;
+    GemvArgs a = {};
+    a.seg[0] = {w, out, rows, 0};
+    a.n_seg = 1;
+    a.x = x;
+    a.cols = cols;
+    launch_gemv(a, EPI_PLAIN, stream);
+}
+
+extern "C" void gemv_residual_forward(bf16 *x, const bf16 *w, const bf16 *in, int rows, int cols,
+                                      bf16 *tap, hipStream_t stream) {
+    if (!check_gemv("gemv_residual", w, in, rows, cols)) return;
+    if (x == in) {
+        llm_fail("gemv_residual: in must not alias x");
+        return;
+    }
+    GemvArgs a = {};
+    a.seg[0] = {w, x, rows, 0};
+    a.n_seg = 1;
+    a.x = in;
+    a.cols = cols;
+    a.tap = tap;
+    launch_gemv(a, EPI_RESID, stream);
+}
+
+extern "C" void qkv_forward(bf16 *q, bf16 *k, bf16 *v, const bf16 *wq, const bf16 *wk,
+                            const bf16 *wv, const bf16 *x, int q_rows, int kv_rows, int cols,
+                            hipStream_t stream) {
+    if (!check_gemv("qkv", wq, x, q_rows, cols) || !check_gemv("qkv", wk, x, kv_rows, cols) ||
+        !check_gemv("qkv", wv, x, kv_rows, cols))
+        return;
+    GemvArgs a = {};
+    a.seg[0] = {wq, q, q_rows, 0};
+    a.seg[1] = {wk, k, kv_rows, 0};
+    a.seg[2] = {wv, v, kv_rows, 0};
+    a.n_seg = 3;
+    a.x = x;
+    a.cols = cols;
+    launch_gemv(a, EPI_PLAIN, stream);
+}
+
+#define GATE_UP_CASES(X) \
+    X(1, 1) X(1, 2) X(1, 4) X(2, 1) X(2, 2) X(2, 4) X(3, 1) X(3, 2) X(4, 1) X(4, 2) X(5, 1) \
+    X(6, 1) X(8, 1) X(10, 1) X(12, 1) X(16, 1) X(20, 1)
+
+extern "C" void gate_up_forward(bf16 *act, const bf16 *w_gate, const bf16 *w_up, const bf16 *x,
+                                int rows, int cols, bf16 *gate_tap, bf16 *up_tap,
+                                hipStream_t stream) {
+    if (!check_gemv("gate_up", w_gate, x, rows, cols) || !check_gemv("gate_up", w_up, x, rows, cols))
+        return;
+    const int nc = pick_nc(cols / 8);
+    const int rpw = pick_rpw(nc, rows, 1);
+    const int waves = (rows + rpw - 1) / rpw;
+    const int blocks = (waves + 3) / 4;
+#define X(NC_, RPW_)                                                                       \
+    if (nc == NC_ && rpw == RPW_) {                                                        \
+        gate_up_kernel<NC_, RPW_><<<blocks, 256, 0, stream>>>(act, w_gate, w_up, x, rows,  \
+                                                             cols, gate_tap, up_tap);      \
+        LAUNCH_OK();                                                                       \
+        return;                                                                            \
+    }
+    GATE_UP_CASES(X)
+#undef X
+    llm_fail("gate_up: no kernel for nc %d rpw %d", nc, rpw);
+}
+
+// ------------------------------------------------------------------------------------------
+// SwiGLU elementwise (src/kernels.cu:283-286 over arrays)
+// ------------------------------------------------------------------------------------------
+
+__device__ __forceinline__ u32x4 swiglu8(const u32x4 &g, const u32x4 &u) {
+    float r[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) r[e] = round_bf(silu_f32(elem(g, e))) * elem(u, e);
+    return u32x4{pack2(r[0], r[1]), pack2(r[2], r[3]), pack2(r[4], r[5]), pack2(r[6], r[7])};
+}
+
+// Grid-stride over 16-byte chunks, four chunks per thread per step so eight loads are in flight.
+__global__ __launch_bounds__(256) void swiglu_kernel(bf16 *act, const bf16 *gate, const bf16 *up,
+                                                     size_t n) {
+    const size_t n_chunks = n / 8;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    size_t c = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (; c + 3 * stride < n_chunks; c += 4 * stride) {
+        u32x4 g[4], u[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            g[i] = ld16_nt(gate + 8 * (c + i * stride));
+            u[i] = ld16_nt(up + 8 * (c + i * stride));
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            __builtin_nontemporal_store(swiglu8(g[i], u[i]), (u32x4 *)(act + 8 * (c + i * stride)));
+    }
+    for (; c < n_chunks; c += stride)
+        __builtin_nontemporal_store(swiglu8(ld16_nt(gate + 8 * c), ld16_nt(up + 8 * c)),
+                                    (u32x4 *)(act + 8 * c));
+    if (blockIdx.x == 0)
+        for (size_t i = n_chunks * 8 + threadIdx.x; i < n; i += blockDim.x)
+            act[i] = (bf16)f2bf(round_bf(silu_f32(bf2f(gate[i]))) * bf2f(up[i]));
+}
+
+// Scalar variant for buffers that are not 16-byte aligned.
+__global__ __launch_bounds__(256) void swiglu_scalar_kernel(bf16 *act, const bf16 *gate,
+                                                            const bf16 *up, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (size_t)gridDim.x * blockDim.x)
+        act[i] = (bf16)f2bf(round_bf(silu_f32(bf2f(gate[i]))) * bf2f(up[i]));
+}
+
+static int device_cus() {
+    static int cus = 0;
+    if (cus == 0) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            cus <= 0)
+            cus = 256;
+    }
+    return cus;
+}
+
+extern "C" void swiglu_forward(bf16 *act, const bf16 *gate, const bf16 *up, size_t n,
+                               hipStream_t stream) {
+    if (n == 0) return;
+    const size_t chunks = (n + 7) / 8;
+    size_t blocks = (chunks + 255) / 256;
+    const size_t cap = (size_t)device_cus() * 8;
+    if (blocks > cap) blocks = cap;
+    if (aligned16(act) && aligned16(gate) && aligned16(up))
+        swiglu_kernel<<<(unsigned)blocks, 256, 0, stream>>>(act, gate, up, n);
+    else
+        swiglu_scalar_kernel<<<(unsigned)blocks, 256, 0, stream>>>(act, gate, up, n);
+    LAUNCH_OK();
+}
+
+// ------------------------------------------------------------------------------------------
+// QK-norm + RoPE + KV-cache write (src/kernels.cu:301-403)
+// ------------------------------------------------------------------------------------------
+
+struct RopeArgs {
+    bf16 *q;
+    bf16 *k;
+    const bf16 *v;
+    const bf16 *qn;
+    const bf16 *kn;
+    bf16 *kc;
+    bf16 *vc;
+    const int *positions;
+    bf16 *q_tap;
+    bf16 *k_tap;
+    int n_tokens, n_heads, n_kv_heads;
+    float eps;
+    int qg, kg, vg;  // waves per token: q head groups, k head groups, v copy groups
+    float inv_freq[128];
+};
+
+// A wave handles 64/(D/16) heads of one token: lane L of a head holds [8L, 8L+8) and
+// [D/2+8L, D/2+8L+8). Sum of squares: fma over the first chunk then the second, tree over the
+// D/16 lanes. The RoPE table (cos/sin of pos*inv_freq_j in double, rounded to fp32 then bf16)
+// is computed one entry per lane and fetched by lane shuffles.
+template <int D>
+__global__ __launch_bounds__(256) void qk_norm_rope_kernel(RopeArgs a) {
+    constexpr int LH = D / 16;
+    constexpr int HPW = 64 / LH;
+    constexpr int HALF = D / 2;
+    constexpr int NJ = (HALF + 63) / 64;
+    const int lane = threadIdx.x & 63;
+    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int per_token = a.qg + a.kg + a.vg;
+    const int t = wave / per_token;
+    if (t >= a.n_tokens) return;
+    const int item = wave - t * per_token;
+    const int pos = a.positions[t];
+    const int hg = lane / LH, L = lane % LH;
+    const int q_dim = a.n_heads * D, kv_dim = a.n_kv_heads * D;
+    const size_t slot = (size_t)pos * kv_dim;
+
+    if (item >= a.qg + a.kg) {  // value rows into the cache
+        const int h = (item - a.qg - a.kg) * HPW + hg;
+        if (h < a.n_kv_heads) {
+            const bf16 *src = a.v + (size_t)t * kv_dim + h * D;
+            bf16 *dst = a.vc + slot + h * D;
+            st16(dst + 8 * L, ld16(src + 8 * L));
+            st16(dst + HALF + 8 * L, ld16(src + HALF + 8 * L));
+        }
+        return;
+    }
+    const bool is_k = item >= a.qg;
+    const int h = (is_k ? item - a.qg : item) * HPW + hg;
+    const bool valid = h < (is_k ? a.n_kv_heads : a.n_heads);
+    const size_t off = (size_t)t * (is_k ? kv_dim : q_dim) + (size_t)h * D;
+    bf16 *x = (is_k ? a.k : a.q) + off;
+    const bf16 *w = is_k ? a.kn : a.qn;
+    bf16 *tap = is_k ? a.k_tap : a.q_tap;
+
+    float cs[NJ], sn[NJ];
+#pragma unroll
+    for (int m = 0; m < NJ; m++) {
+        const int j = lane + 64 * m;
+        cs[m] = sn[m] = 0.0f;
+        if (j < HALF) {
+            const float angle = (float)pos * a.inv_freq[j];
+            double s, c;
+            sincos_d((double)angle, &s, &c);
+            cs[m] = round_bf((float)c);
+            sn[m] = round_bf((float)s);
+        }
+    }
+
+    u32x4 xa = {0, 0, 0, 0}, xb = {0, 0, 0, 0};
+    if (valid) {
+        xa = ld16(x + 8 * L);
+        xb = ld16(x + HALF + 8 * L);
+    }
+    const u32x4 wa = ld16(w + 8 * L), wb = ld16(w + HALF + 8 * L);
+    float acc = dot8(xa, xa, 0.0f);
+    acc = dot8(xb, xb, acc);
+    const float total = group_sum<LH>(acc);
+    const float inv = 1.0f / sqrtf(total / (float)D + a.eps);
+    float ya[8], yb[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        ya[e] = round_bf(round_bf(elem(xa, e) * inv) * elem(wa, e));
+        yb[e] = round_bf(round_bf(elem(xb, e) * inv) * elem(wb, e));
+    }
+    if (valid && tap) {
+        st16(tap + off + 8 * L, u32x4{pack2(ya[0], ya[1]), pack2(ya[2], ya[3]),
+                                      pack2(ya[4], ya[5]), pack2(ya[6], ya[7])});
+        st16(tap + off + HALF + 8 * L, u32x4{pack2(yb[0], yb[1]), pack2(yb[2], yb[3]),
+                                             pack2(yb[4], yb[5]), pack2(yb[6], yb[7])});
+    }
+    float oa[8], ob[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const int j = 8 * L + e;
+        float c = __shfl(cs[0], j & 63), s = __shfl(sn[0], j & 63);
+#pragma unroll
+        for (int m = 1; m < NJ; m++) {
+            const float cm = __shfl(cs[m], j & 63), sm = __shfl(sn[m], j & 63);
+            if ((j >> 6) == m) {
+                c = cm;
+                s = sm;
+            }
+        }
+        const float a_cos = round_bf(ya[e] * c);
+        const float b_sin = round_bf(yb[e] * s);
+        const float b_cos = round_bf(yb[e] * c);
+        const float a_sin = round_bf(ya[e] * s);
+        oa[e] = a_cos - b_sin;
+        ob[e] = b_cos + a_sin;
+    }
+    if (valid) {
+        const u32x4 va = {pack2(oa[0], oa[1]), pack2(oa[2], oa[3]), pack2(oa[4], oa[5]),
+                          pack2(oa[6], oa[7])};
+        const u32x4 vb = {pack2(ob[0], ob[1]), pack2(ob[2], ob[3]), pack2(ob[4], ob[5]),
+                          pack2(ob[6], ob[7])};
+        st16(x + 8 * L, va);
+        st16(x + HALF + 8 * L, vb);
+        if (is_k) {
+            st16(a.kc + slot + h * D + 8 * L, va);
+            st16(a.kc + slot + h * D + HALF + 8 * L, vb);
+        }
+    }
+}
+
+// inv_freq_j = 1 / fp32(pow(theta, fp32(2j / D))) as HF computes it (modeling_qwen3.py:121),
+// cached per (theta, D).
+static void rope_inv_freq(float theta, int D, float *out) {
+    static std::mutex mu;
+    static float cached_theta = -1.0f;
+    static int cached_d = -1;
+    static float table[128];
+    std::lock_guard<std::mutex> lock(mu);
+    if (cached_theta != theta || cached_d != D) {
+        for (int j = 0; j < D / 2; j++) {
+            const float e = (float)(2 * j) / (float)D;
+            table[j] = 1.0f / (float)pow((double)theta, (double)e);
+        }
+        cached_theta = theta;
+        cached_d = D;
+    }
+    memcpy(out, table, sizeof(float) * (D / 2));
+}
+
+static void launch_qk_norm_rope(bf16 *q, bf16 *k, const bf16 *v, const bf16 *q_norm_w,
+                                const bf16 *k_norm_w, bf16 *key_cache, bf16 *value_cache,
+                                const int *positions, int n_tokens, int n_heads, int n_kv_heads,
+                                int head_dim, float eps, float theta, bf16 *q_tap, bf16 *k_tap,
+                                hipStream_t stream) {
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256) {
+        llm_fail("qk_norm_rope: head_dim %d is not 64, 128 or 256", head_dim);
+        return;
+    }
+    if (n_tokens <= 0 || n_heads <= 0 || n_kv_heads <= 0) {
+        llm_fail("qk_norm_rope: n_tokens %d, n_heads %d, n_kv_heads %d must be positive",
+                 n_tokens, n_heads, n_kv_heads);
+        return;
+    }
+    const void *ptrs[] = {q, k, v, q_norm_w, k_norm_w, key_cache, value_cache, q_tap, k_tap};
+    for (const void *p : ptrs)
+        if (p && !aligned16(p)) {
+            llm_fail("qk_norm_rope: tensors must be 16-byte aligned");
+            return;
+        }
+    RopeArgs a;
+    memset(&a, 0, sizeof a);
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.qn = q_norm_w;
+    a.kn = k_norm_w;
+    a.kc = key_cache;
+    a.vc = value_cache;
+    a.positions = positions;
+    a.q_tap = q_tap;
+    a.k_tap = k_tap;
+    a.n_tokens = n_tokens;
+    a.n_heads = n_heads;
+    a.n_kv_heads = n_kv_heads;
+    a.eps = eps;
+    const int hpw = 64 / (head_dim / 16);
+    a.qg = (n_heads + hpw - 1) / hpw;
+    a.kg = (n_kv_heads + hpw - 1) / hpw;
+    a.vg = a.kg;
+    rope_inv_freq(theta, head_dim, a.inv_freq);
+    const long waves = (long)n_tokens * (a.qg + a.kg + a.vg);
+    const unsigned blocks = (unsigned)((waves + 3) / 4);
+    if (head_dim == 64)
+        qk_norm_rope_kernel<64><<<blocks, 256, 0, stream>>>(a);
+    else if (head_dim == 128)
+        qk_norm_rope_kernel<128><<<blocks, 256, 0, stream>>>(a);
+    else
+        qk_norm_rope_kernel<256><<<blocks, 256, 0, stream>>>(a);
+    LAUNCH_OK();
+}
+
+extern "C" void qk_norm_rope_forward(bf16 *q, bf16 *k, const bf16 *v, const bf16 *q_norm_w,
+                                     const bf16 *k_norm_w, bf16 *key_cache, bf16 *value_cache,
+                                     const int *d_pos, int n_heads, int n_kv_heads, int head_dim,
+                                     float eps, float theta, bf16 *q_tap, bf16 *k_tap,
+                                     hipStream_t stream) {
+    launch_qk_norm_rope(q, k, v, q_norm_w, k_norm_w, key_cache, value_cache, d_pos, 1, n_heads,
+                        n_kv_heads, head_dim, eps, theta, q_tap, k_tap, stream);
+}
+
+extern "C" void qk_norm_rope_rows(bf16 *q, bf16 *k, const bf16 *v, const bf16 *q_norm_w,
+                                  const bf16 *k_norm_w, bf16 *key_cache, bf16 *value_cache,
+                                  const int *d_positions, int n_tokens, int n_heads,
+                                  int n_kv_heads, int head_dim, float eps, float theta,
+                                  bf16 *q_tap, bf16 *k_tap, hipStream_t stream) {
+    launch_qk_norm_rope(q, k, v, q_norm_w, k_norm_w, key_cache, value_cache, d_positions,
+                        n_tokens, n_heads, n_kv_heads, head_dim, eps, theta, q_tap, k_tap, stream);
+}
+
+// ------------------------------------------------------------------------------------------
+// decode attention, split softmax (src/kernels.cu:439-497)
+// ------------------------------------------------------------------------------------------
+
+constexpr int ATT_B = 64;  // positions per block
+
+struct AttnArgs {
+    bf16 *out;
+    const bf16 *q;
+    const bf16 *kc;
+    const bf16 *vc;
+    float *scores;   // [n_heads, max_seq]
+    float *stats;    // [n_heads, max_blocks, 2]: block max, block sum of exp(s - max)
+    float *partial;  // [n_heads, max_blocks, D]: block sums of p v
+    const int *d_pos;
+    int n_heads, n_kv_heads, max_seq, max_blocks;
+    float scale;
+};
+
+static size_t ceil_div(size_t a, size_t b) { return (a + b - 1) / b; }
+
+extern "C" size_t attention_workspace_floats(int n_heads, int head_dim, int max_seq) {
+    const size_t mb = ceil_div((size_t)max_seq, ATT_B);
+    return (size_t)n_heads * max_seq + (size_t)n_heads * mb * (2 + (size_t)head_dim);
+}
+
+// Pass 1, per (block of 64 positions, kv head): scores of the REP query heads sharing the kv
+// head, s = bf16(bf16(q.k) * scale) with q.k over D/8 lanes; then per head the block max and
+// the block's tree sum of exp(s - max). Work items are strided over a fixed grid because the
+// position count is only known on the device.
+template <int D, int REP>
+__global__ __launch_bounds__(256) void attn_scores_kernel(AttnArgs a) {
+    constexpr int LP = D / 8, PPW = 64 / LP, PER_WAVE = ATT_B / 4, ITERS = PER_WAVE / PPW;
+    __shared__ float sc[REP][ATT_B];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int G = lane / LP, L = lane % LP;
+    const int n = *a.d_pos + 1;
+    const int nb = (n + ATT_B - 1) / ATT_B;
+    const int kv_dim = a.n_kv_heads * D;
+    for (int item = blockIdx.x; item < nb * a.n_kv_heads; item += gridDim.x) {
+        const int b = item / a.n_kv_heads, g = item - b * a.n_kv_heads;
+        u32x4 qv[REP];
+#pragma unroll
+        for (int r = 0; r < REP; r++) qv[r] = ld16(a.q + (size_t)(g * REP + r) * D + 8 * L);
+        u32x4 kv[ITERS];
+#pragma unroll
+        for (int it = 0; it < ITERS; it++) {
+            const int t = b * ATT_B + w * PER_WAVE + it * PPW + G;
+            kv[it] = t < n ? ld16_nt(a.kc + (size_t)t * kv_dim + g * D + 8 * L) : u32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int it = 0; it < ITERS; it++) {
+            const int slot = w * PER_WAVE + it * PPW + G;
+            const int t = b * ATT_B + slot;
+#pragma unroll
+            for (int r = 0; r < REP; r++) {
+                const float d = group_sum<LP>(dot8(qv[r], kv[it], 0.0f));
+                const float s = round_bf(round_bf(d) * a.scale);
+                if (L == 0) {
+                    sc[r][slot] = s;
+                    if (t < n) a.scores[(size_t)(g * REP + r) * a.max_seq + t] = s;
+                }
+            }
+        }
+        __syncthreads();
+        for (int r = w; r < REP; r += 4) {
+            const bool v = b * ATT_B + lane < n;
+            const float s = v ? sc[r][lane] : -__builtin_huge_valf();
+            const float m = wave_max(s);
+            const float e = v ? exp_f32(s - m) : 0.0f;
+            const float S = wave_sum(e);
+            if (lane == 0) {
+                float *st = a.stats + ((size_t)(g * REP + r) * a.max_blocks + b) * 2;
+                st[0] = m;
+                st[1] = S;
+            }
+        }
+        __syncthreads();
+    }
+}
+
+// Pass 2, per (block, kv head): each query head's global max M and sum (chunks of 64 block
+// statistics: tree sum of S_b exp(m_b - M), chunks added in order), the block's probabilities
+// p = bf16(exp(s - M) / sum), then p v accumulated per lane over its positions, tree over the
+// position groups of a wave, waves added in order 0..3.
+template <int D, int REP>
+__global__ __launch_bounds__(256) void attn_pv_kernel(AttnArgs a) {
+    constexpr int LP = D / 8, PPW = 64 / LP, PER_WAVE = ATT_B / 4, ITERS = PER_WAVE / PPW;
+    __shared__ float p_s[REP][ATT_B];
+    __shared__ float red[4][REP][D];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int G = lane / LP, L = lane % LP;
+    const int n = *a.d_pos + 1;
+    const int nb = (n + ATT_B - 1) / ATT_B;
+    const int kv_dim = a.n_kv_heads * D;
+    for (int item = blockIdx.x; item < nb * a.n_kv_heads; item += gridDim.x) {
+        const int b = item / a.n_kv_heads, g = item - b * a.n_kv_heads;
+        u32x4 vv[ITERS];
+#pragma unroll
+        for (int it = 0; it < ITERS; it++) {
+            const int t = b * ATT_B + w * PER_WAVE + it * PPW + G;
+            vv[it] = t < n ? ld16_nt(a.vc + (size_t)t * kv_dim + g * D + 8 * L) : u32x4{0, 0, 0, 0};
+        }
+        for (int r = w; r < REP; r += 4) {
+            const int h = g * REP + r;
+            const float *st = a.stats + (size_t)h * a.max_blocks * 2;
+            float M = -__builtin_huge_valf();
+            for (int c0 = 0; c0 < nb; c0 += 64) {
+                const int bi = c0 + lane;
+                M = fmaxf(M, wave_max(bi < nb ? st[2 * bi] : -__builtin_huge_valf()));
+            }
+            float sum = 0.0f;
+            for (int c0 = 0; c0 < nb; c0 += 64) {
+                const int bi = c0 + lane;
+                const float term = bi < nb ? st[2 * bi + 1] * exp_f32(st[2 * bi] - M) : 0.0f;
+                const float cs = wave_sum(term);
+                sum = c0 == 0 ? cs : sum + cs;
+            }
+            const int t = b * ATT_B + lane;
+            p_s[r][lane] =
+                t < n ? round_bf(exp_f32(a.scores[(size_t)h * a.max_seq + t] - M) / sum) : 0.0f;
+        }
+        __syncthreads();
+        float acc[REP][8];
+#pragma unroll
+        for (int r = 0; r < REP; r++)
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc[r][e] = 0.0f;
+#pragma unroll
+        for (int it = 0; it < ITERS; it++) {
+            const int slot = w * PER_WAVE + it * PPW + G;
+            if (b * ATT_B + slot < n) {
+#pragma unroll
+                for (int r = 0; r < REP; r++) {
+                    const float p = p_s[r][slot];
+#pragma unroll
+                    for (int e = 0; e < 8; e++) acc[r][e] = fmaf(p, elem(vv[it], e), acc[r][e]);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < REP; r++)
+#pragma unroll
+            for (int e = 0; e < 8; e++)
+#pragma unroll
+                for (int s = LP; s < 64; s <<= 1) acc[r][e] += __shfl_xor(acc[r][e], s);
+        if (G == 0)
+#pragma unroll
+            for (int r = 0; r < REP; r++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) red[w][r][8 * L + e] = acc[r][e];
+        __syncthreads();
+        for (int i = threadIdx.x; i < REP * D; i += 256) {
+            const int r = i / D, d = i - r * D;
+            const float v = ((red[0][r][d] + red[1][r][d]) + red[2][r][d]) + red[3][r][d];
+            a.partial[((size_t)(g * REP + r) * a.max_blocks + b) * D + d] = v;
+        }
+        __syncthreads();
+    }
+}
+
+// Pass 3: out = bf16(block partials added in block order).
+template <int D>
+__global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
+    const int h = blockIdx.x;
+    const int n = *a.d_pos + 1;
+    const int nb = (n + ATT_B - 1) / ATT_B;
+    for (int d = threadIdx.x; d < D; d += blockDim.x) {
+        const float *p = a.partial + (size_t)h * a.max_blocks * D + d;
+        float acc = p[0];
+        for (int b = 1; b < nb; b++) acc = acc + p[(size_t)b * D];
+        a.out[(size_t)h * D + d] = (bf16)f2bf(acc);
+    }
+}
+
+template <int D, int REP>
+static void launch_attention_t(const AttnArgs &a, int grid, hipStream_t stream) {
+    attn_scores_kernel<D, REP><<<grid, 256, 0, stream>>>(a);
+    if (!LAUNCH_OK()) return;
+    attn_pv_kernel<D, REP><<<grid, 256, 0, stream>>>(a);
+    if (!LAUNCH_OK()) return;
+    attn_combine_kernel<D><<<a.n_heads, D < 256 ? D : 256, 0, stream>>>(a);
+    LAUNCH_OK();
+}
+
+extern "C" void attention_forward(bf16 *out, const bf16 *q, const bf16 *key_cache,
+                                  const bf16 *value_cache, float *att, int n_heads, int n_kv_heads,
+                                  int head_dim, const int *d_pos, int max_seq, float scale,
+                                  hipStream_t stream) {
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256) {
+        llm_fail("attention: head_dim %d is not 64, 128 or 256", head_dim);
+        return;
+    }
+    if (n_kv_heads <= 0 || n_heads % n_kv_heads != 0) {
+        llm_fail("attention: n_heads %d is not a multiple of n_kv_heads %d", n_heads, n_kv_heads);
+        return;
+    }
+    const int rep = n_heads / n_kv_heads;
+    if (rep != 1 && rep != 2 && rep != 4 && rep != 8) {
+        llm_fail("attention: n_heads / n_kv_heads = %d is not 1, 2, 4 or 8", rep);
+        return;
+    }
+    if (max_seq <= 0) {
+        llm_fail("attention: max_seq %d must be positive", max_seq);
+        return;
+    }
+    if (!aligned16(q) || !aligned16(key_cache) || !aligned16(value_cache)) {
+        llm_fail("attention: q and the caches must be 16-byte aligned");
+        return;
+    }
+    AttnArgs a;
+    a.out = out;
+    a.q = q;
+    a.kc = key_cache;
+    a.vc = value_cache;
+    a.max_blocks = (int)ceil_div((size_t)max_seq, ATT_B);
+    a.scores = att;
+    a.stats = att + (size_t)n_heads * max_seq;
+    a.partial = a.stats + (size_t)n_heads * a.max_blocks * 2;
+    a.d_pos = d_pos;
+    a.n_heads = n_heads;
+    a.n_kv_heads = n_kv_heads;
+    a.max_seq = max_seq;
+    a.scale = scale;
+    long items = (long)a.max_blocks * n_kv_heads;
+    const int grid = (int)(items < 1024 ? items : 1024);
+#define ATT(D_, R_)                                    \
+    if (head_dim == D_ && rep == R_) {                 \
+        launch_attention_t<D_, R_>(a, grid, stream);   \
+        return;                                        \
+    }
+    ATT(64, 1) ATT(64, 2) ATT(64, 4) ATT(64, 8) ATT(128, 1) ATT(128, 2) ATT(128, 4) ATT(128, 8)
+    ATT(256, 1) ATT(256, 2) ATT(256, 4) ATT(256, 8)
+#undef ATT
+}
+
+// ------------------------------------------------------------------------------------------
+// argmax (src/kernels.cu:499-544), two stages
+// ------------------------------------------------------------------------------------------
+
+constexpr int AMAX_GROUPS = 256;
+// Library-owned partial results of argmax_forward (calls on one device must not overlap).
+__device__ float g_amax_val[AMAX_GROUPS];
+__device__ int g_amax_idx[AMAX_GROUPS];
+
+// Larger value wins, equal values keep the lower index; NaN is never taken.
+__device__ __forceinline__ void amax_pair(float &v, int &i, float v2, int i2) {
+    if (v2 > v || (v2 == v && i2 < i)) {
+        v = v2;
+        i = i2;
+    }
+}
+
+__device__ __forceinline__ void block_amax(float &v, int &i, float *lv, int *li) {
+#pragma unroll
+    for (int s = 1; s < 64; s <<= 1) {
+        const float v2 = __shfl_xor(v, s);
+        const int i2 = __shfl_xor(i, s);
+        amax_pair(v, i, v2, i2);
+    }
+    const int w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        lv[w] = v;
+        li[w] = i;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0)
+        for (int k = 1; k < (int)(blockDim.x >> 6); k++) amax_pair(v, i, lv[k], li[k]);
+}
+
+__global__ __launch_bounds__(256) void argmax_stage1_kernel(const bf16 *x, int n, int vec,
+                                                            float *pv, int *pi) {
+    __shared__ float lv[4];
+    __shared__ int li[4];
+    float v = -__builtin_huge_valf();
+    int idx = INT_MAX;
+    const int stride = gridDim.x * blockDim.x;
+    const int t0 = blockIdx.x * blockDim.x + threadIdx.x;
+    int done = 0;
+    if (vec) {
+        const int n_chunks = n / 8;
+        for (int c = t0; c < n_chunks; c += stride) {
+            const u32x4 ch = ld16(x + 8 * (size_t)c);
+#pragma unroll
+            for (int e = 0; e < 8; e++) amax_pair(v, idx, elem(ch, e), 8 * c + e);
+        }
+        done = n_chunks * 8;
+    }
+    for (int i = done + t0; i < n; i += stride) amax_pair(v, idx, bf2f(x[i]), i);
+    block_amax(v, idx, lv, li);
+    if (threadIdx.x == 0) {
+        pv[blockIdx.x] = v;
+        pi[blockIdx.x] = idx;
+    }
+}
+
+__global__ __launch_bounds__(256) void argmax_stage2_kernel(const float *pv, const int *pi,
+                                                            int groups, int *out) {
+    __shared__ float lv[4];
+    __shared__ int li[4];
+    float v = -__builtin_huge_valf();
+    int idx = INT_MAX;
+    for (int k = threadIdx.x; k < groups; k += blockDim.x) amax_pair(v, idx, pv[k], pi[k]);
+    block_amax(v, idx, lv, li);
+    if (threadIdx.x == 0) *out = idx;
+}
+
+int argmax_partial_count() { return AMAX_GROUPS; }
+
+static int argmax_groups(int n) {
+    const int g = (n + 256 * 8 - 1) / (256 * 8);
+    return g < 1 ? 1 : (g > AMAX_GROUPS ? AMAX_GROUPS : g);
+}
+
+// Shared by argmax_forward (library buffer) and the step (its own buffer).
+void argmax_launch(int *out, const bf16 *x, int n, float *pv, int *pi, hipStream_t stream) {
+    const int groups = argmax_groups(n);
+    argmax_stage1_kernel<<<groups, 256, 0, stream>>>(x, n, aligned16(x) ? 1 : 0, pv, pi);
+    if (!LAUNCH_OK()) return;
+    argmax_stage2_kernel<<<1, 256, 0, stream>>>(pv, pi, groups, out);
+    LAUNCH_OK();
+}
+
+extern "C" void argmax_forward(int *out, const bf16 *x, int n, hipStream_t stream) {
+    if (n <= 0) {
+        llm_fail("argmax: n %d must be positive", n);
+        return;
+    }
+    // Each device holds its own copy of the partials; look their addresses up once per device.
+    static std::mutex mu;
+    static float *pv_dev[64];
+    static int *pi_dev[64];
+    int dev = 0;
+    if (!HIP_OK(hipGetDevice(&dev))) return;
+    if (dev < 0 || dev >= 64) {
+        llm_fail("argmax: device %d out of range", dev);
+        return;
+    }
+    float *pv;
+    int *pi;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        if (!pv_dev[dev]) {
+            if (!HIP_OK(hipGetSymbolAddress((void **)&pv_dev[dev], HIP_SYMBOL(g_amax_val))) ||
+                !HIP_OK(hipGetSymbolAddress((void **)&pi_dev[dev], HIP_SYMBOL(g_amax_idx)))) {
+                pv_dev[dev] = nullptr;
+                return;
+            }
+        }
+        pv = pv_dev[dev];
+        pi = pi_dev[dev];
+    }
+    argmax_launch(out, x, n, pv, pi, stream);
+}

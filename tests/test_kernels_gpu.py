@@ -1,0 +1,303 @@
+"""Parity of every HIP launcher with the CPU oracle on the same seeded inputs.
+
+GPU results must be bit-identical to the oracle's GPU-order mode (same fp32 operations in the
+same order) and within the north-star tolerance of its exact mode: 1 bf16 ulp for RMSNorm,
+RoPE and SwiGLU, bit-exact for the embedding rows, KV-cache slots and argmax. Shapes are the
+Qwen3-0.6B decode layer (hidden 1024, 16q/8kv heads of 128, intermediate 3072, vocab 151936),
+the Qwen3-4B widths (2560, 32/8, 9728) and the many-row roofline sweep sizes, plus ragged and
+tiny edge cases."""
+import math
+
+import numpy as np
+import pytest
+
+from conftest import (bf16_bits, bf16_ulp_diff, bf16_vals, rand_bf16, ulp_bf16,
+                      within_one_ulp_then_scale)
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(bits):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(bits, dtype=np.uint16).view(np.int16)).cuda()
+
+
+def host(t):
+    import torch
+    torch.cuda.synchronize()
+    return t.cpu().numpy().view(np.uint16)
+
+
+def dev_i32(a):
+    import torch
+    return torch.tensor(np.asarray(a, dtype=np.int32)).cuda()
+
+
+def ident(name):
+    print(f"[case] {name}", flush=True)
+
+
+# ---------------------------------------------------------------- embedding
+
+def test_embedding_rows_bit_exact(gpu, oracle):
+    import torch
+    ident("embedding 151936x1024 and 1000x2560")
+    rng = np.random.default_rng(20)
+    for vocab, hidden in [(151936, 1024), (1000, 2560), (50, 20)]:
+        table = torch.randn(vocab, hidden, device="cuda").to(torch.bfloat16).view(torch.int16)
+        for tok in [0, 1, vocab // 2, vocab - 1, int(rng.integers(0, vocab))]:
+            out = torch.zeros(hidden, dtype=torch.int16, device="cuda")
+            gpu.embedding_forward(out, table, dev_i32([tok]), hidden)
+            assert np.array_equal(host(out), host(table[tok]))
+
+
+# ---------------------------------------------------------------- RMSNorm
+
+@pytest.mark.parametrize("rows,dim", [(1, 1024), (1, 2560), (4096, 2560), (3, 100), (2, 9000),
+                                      (5, 8200), (7, 8192), (1, 8)])
+def test_rmsnorm(gpu, oracle, rows, dim):
+    ident(f"rmsnorm {rows}x{dim}")
+    rng = np.random.default_rng(rows * 7 + dim)
+    x = rand_bf16(rng, (rows, dim))
+    w = rand_bf16(rng, dim, 0.1, 1.0)
+    out = dev(np.zeros((rows, dim), np.uint16))
+    gpu.rmsnorm_forward(out, dev(x), dev(w), rows, dim, 1e-6)
+    y = host(out).reshape(rows, dim)
+    assert np.array_equal(y, oracle.rmsnorm(x, w, 1e-6, oracle.GPU_ORDER))
+    n_exact = oracle.rmsnorm(x, bf16_bits(np.ones(dim)), 1e-6, oracle.EXACT)
+    assert within_one_ulp_then_scale(y, n_exact, w).all()
+
+
+# ---------------------------------------------------------------- GEMV family
+
+GEMV_SHAPES = [(4096, 1024), (1024, 2048), (1024, 3072), (2560, 9728), (2560, 4096),
+               (151936, 1024), (37, 520), (5, 8), (3, 16400)]
+
+
+@pytest.mark.parametrize("rows,cols", GEMV_SHAPES)
+def test_gemv(gpu, oracle, rows, cols):
+    ident(f"gemv {rows}x{cols}")
+    rng = np.random.default_rng(rows + cols)
+    w = rand_bf16(rng, (rows, cols), 0.02)
+    x = rand_bf16(rng, cols)
+    out = dev(np.zeros(rows, np.uint16))
+    gpu.gemv_forward(out, dev(w), dev(x), rows, cols)
+    y = host(out)
+    assert np.array_equal(y, oracle.gemv(w, x, oracle.GPU_ORDER))
+    # against exact arithmetic: one bf16 ulp after the single rounding, plus the fp32
+    # accumulation bound 2 * cols * 2^-24 * sum|w x|
+    wv, xv = bf16_vals(w).astype(np.float64), bf16_vals(x).astype(np.float64)
+    exact = wv @ xv
+    bound = ulp_bf16(exact) + 2 * cols * 2.0 ** -24 * (np.abs(wv) @ np.abs(xv))
+    assert np.all(np.abs(bf16_vals(y) - exact) <= bound)
+
+
+@pytest.mark.parametrize("rows,cols", [(1024, 2048), (1024, 3072), (2560, 4096), (2560, 9728),
+                                       (33, 64)])
+def test_gemv_residual(gpu, oracle, rows, cols):
+    ident(f"gemv_residual {rows}x{cols}")
+    rng = np.random.default_rng(rows * 3 + cols)
+    w = rand_bf16(rng, (rows, cols), 0.02)
+    inp = rand_bf16(rng, cols)
+    x = rand_bf16(rng, rows)
+    xd, tap = dev(x), dev(np.zeros(rows, np.uint16))
+    gpu.gemv_residual_forward(xd, dev(w), dev(inp), rows, cols, tap)
+    ex, et = oracle.gemv_residual(x, w, inp, oracle.GPU_ORDER, with_tap=True)
+    assert np.array_equal(host(tap), et)
+    assert np.array_equal(host(xd), ex)
+    xd = dev(x)
+    gpu.gemv_residual_forward(xd, dev(w), dev(inp), rows, cols, None)
+    assert np.array_equal(host(xd), ex)
+
+
+@pytest.mark.parametrize("hq,hkv,H", [(16, 8, 1024), (32, 8, 2560), (3, 1, 64)])
+def test_qkv(gpu, oracle, hq, hkv, H):
+    ident(f"qkv {hq}/{hkv} x {H}")
+    rng = np.random.default_rng(hq + H)
+    wq = rand_bf16(rng, (hq * 128, H), 0.02)
+    wk = rand_bf16(rng, (hkv * 128, H), 0.02)
+    wv = rand_bf16(rng, (hkv * 128, H), 0.02)
+    x = rand_bf16(rng, H)
+    q, k, v = (dev(np.zeros(n, np.uint16)) for n in (hq * 128, hkv * 128, hkv * 128))
+    gpu.qkv_forward(q, k, v, dev(wq), dev(wk), dev(wv), dev(x), hq * 128, hkv * 128, H)
+    eq, ek, ev = oracle.qkv(wq, wk, wv, x, oracle.GPU_ORDER)
+    assert np.array_equal(host(q), eq)
+    assert np.array_equal(host(k), ek)
+    assert np.array_equal(host(v), ev)
+
+
+@pytest.mark.parametrize("rows,cols", [(3072, 1024), (6144, 2048), (9728, 2560), (77, 136)])
+def test_gate_up(gpu, oracle, rows, cols):
+    ident(f"gate_up {rows}x{cols}")
+    rng = np.random.default_rng(rows + 5 * cols)
+    wg = rand_bf16(rng, (rows, cols), 0.02)
+    wu = rand_bf16(rng, (rows, cols), 0.02)
+    x = rand_bf16(rng, cols)
+    act, gt, ut = (dev(np.zeros(rows, np.uint16)) for _ in range(3))
+    gpu.gate_up_forward(act, dev(wg), dev(wu), dev(x), rows, cols, gt, ut)
+    ea, eg, eu = oracle.gate_up(wg, wu, x, oracle.GPU_ORDER, with_taps=True)
+    assert np.array_equal(host(gt), eg) and np.array_equal(host(ut), eu)
+    assert np.array_equal(host(act), ea)
+    s_exact = oracle.swiglu(eg, bf16_bits(np.ones(rows)), oracle.EXACT)
+    assert within_one_ulp_then_scale(host(act), s_exact, eu).all()
+    act2 = dev(np.zeros(rows, np.uint16))
+    gpu.gate_up_forward(act2, dev(wg), dev(wu), dev(x), rows, cols, None, None)
+    assert np.array_equal(host(act2), ea)
+
+
+# ---------------------------------------------------------------- SwiGLU
+
+@pytest.mark.parametrize("n", [65280, 4096 * 9728, 1001, 7])
+def test_swiglu(gpu, oracle, n):
+    ident(f"swiglu n={n}")
+    rng = np.random.default_rng(n)
+    if n == 65280:  # every finite bf16 gate value
+        g = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+        g = g[np.isfinite(bf16_vals(g))]
+    else:
+        g = rand_bf16(rng, n, 2.0)
+    u = rand_bf16(rng, g.size)
+    act = dev(np.zeros(g.size, np.uint16))
+    gpu.swiglu_forward(act, dev(g), dev(u), g.size)
+    y = host(act)
+    assert np.array_equal(y, oracle.swiglu(g, u, oracle.GPU_ORDER))
+    s_exact = oracle.swiglu(g, bf16_bits(np.ones(g.size)), oracle.EXACT)
+    assert within_one_ulp_then_scale(y, s_exact, u).all()
+
+
+# ---------------------------------------------------------------- QK-norm + RoPE + KV write
+
+def rope_rotate(tap, positions, D, theta, oracle):
+    """HF's apply_rotary_pos_emb on bf16 heads, computed independently: angles fp32(pos *
+    inv_freq_j) (inv_freq pinned to decimal arithmetic), cos/sin from libm rounded through fp32
+    to bf16, each product and the sum rounded to bf16 (modeling_qwen3.py:126-170)."""
+    inv = oracle.inv_freq(theta, D)
+    T = len(positions)
+    y = bf16_vals(np.asarray(tap, dtype=np.uint16).reshape(T, -1, D))
+    out = np.empty(y.shape, np.uint16)
+    r = lambda z: bf16_vals(bf16_bits(z))
+    for t, p in enumerate(positions):
+        ang = (np.float32(p) * inv).astype(np.float32)
+        c = bf16_vals(bf16_bits(np.array([math.cos(float(a)) for a in ang], np.float32)))
+        s = bf16_vals(bf16_bits(np.array([math.sin(float(a)) for a in ang], np.float32)))
+        a, b = y[t, :, :D // 2], y[t, :, D // 2:]
+        out[t, :, :D // 2] = bf16_bits(r(a * c) - r(b * s))
+        out[t, :, D // 2:] = bf16_bits(r(b * c) + r(a * s))
+    return out
+
+
+def _rope_case(rng, n_tokens, hq, hkv, D, max_seq):
+    q = rand_bf16(rng, (n_tokens, hq * D))
+    k = rand_bf16(rng, (n_tokens, hkv * D))
+    v = rand_bf16(rng, (n_tokens, hkv * D))
+    qn = rand_bf16(rng, D, 0.1, 1.0)
+    kn = rand_bf16(rng, D, 0.1, 1.0)
+    kc = np.full((max_seq, hkv * D), 0x7FC1, np.uint16)
+    vc = np.full((max_seq, hkv * D), 0x7FC3, np.uint16)
+    return q, k, v, qn, kn, kc, vc
+
+
+@pytest.mark.parametrize("hq,hkv,D,pos", [(16, 8, 128, 0), (16, 8, 128, 1), (16, 8, 128, 3071),
+                                          (32, 8, 128, 4095), (4, 2, 64, 77), (4, 2, 256, 500),
+                                          (3, 1, 128, 9)])
+def test_qk_norm_rope_decode(gpu, oracle, hq, hkv, D, pos):
+    """Config-1 decode: q/k rotated in place bit-exactly, k'/v written to cache row pos only."""
+    ident(f"qk_norm_rope decode {hq}/{hkv} D{D} pos{pos}")
+    rng = np.random.default_rng(hq * 1000 + pos)
+    max_seq = 4096
+    q, k, v, qn, kn, kc, vc = _rope_case(rng, 1, hq, hkv, D, max_seq)
+    qd, kd, kcd, vcd = dev(q), dev(k), dev(kc), dev(vc)
+    qt, kt = dev(np.zeros_like(q)), dev(np.zeros_like(k))
+    gpu.qk_norm_rope_forward(qd, kd, dev(v), dev(qn), dev(kn), kcd, vcd, dev_i32([pos]), hq, hkv,
+                             D, 1e-6, 1e6, qt, kt)
+    eq, ek, ekc, evc, eqt, ekt = oracle.qk_norm_rope_rows(q, k, v, qn, kn, kc, vc, [pos], hq, hkv,
+                                                          D, 1e-6, 1e6, oracle.GPU_ORDER,
+                                                          with_taps=True)
+    assert np.array_equal(host(qt).reshape(eqt.shape), eqt)
+    assert np.array_equal(host(kt).reshape(ekt.shape), ekt)
+    assert np.array_equal(host(qd).reshape(eq.shape), eq)
+    assert np.array_equal(host(kd).reshape(ek.shape), ek)
+    gkc, gvc = host(kcd).reshape(kc.shape), host(vcd).reshape(vc.shape)
+    assert np.array_equal(gkc, ekc) and np.array_equal(gvc, evc)
+    assert np.array_equal(gkc[pos], host(kd).reshape(-1)) and np.array_equal(gvc[pos], v[0])
+    # tolerance against exact arithmetic: the normed heads within 1 ulp at HF's rounding point,
+    # and the rotation of the GPU's own normed heads bit-exact against libm cos/sin
+    ones = bf16_bits(np.ones(D))
+    nq = oracle.qk_norm_rope_rows(q, k, v, ones, ones, kc, vc, [pos], hq, hkv, D, 1e-6, 1e6,
+                                  oracle.EXACT, with_taps=True)
+    assert within_one_ulp_then_scale(host(qt).reshape(-1), nq[4].reshape(-1), np.tile(qn, hq)).all()
+    assert within_one_ulp_then_scale(host(kt).reshape(-1), nq[5].reshape(-1), np.tile(kn, hkv)).all()
+    assert np.array_equal(host(qd).reshape(-1), rope_rotate(host(qt), [pos], D, 1e6, oracle).reshape(-1))
+    assert np.array_equal(host(kd).reshape(-1), rope_rotate(host(kt), [pos], D, 1e6, oracle).reshape(-1))
+
+
+def test_qk_norm_rope_rows_sweep(gpu, oracle):
+    """Config-5 sweep: 4096 tokens x (32 q + 8 kv) heads of 128 at positions 0..4095."""
+    ident("qk_norm_rope rows 4096 tokens 32/8")
+    rng = np.random.default_rng(30)
+    T, hq, hkv, D = 4096, 32, 8, 128
+    q, k, v, qn, kn, kc, vc = _rope_case(rng, T, hq, hkv, D, T)
+    pos = np.arange(T, dtype=np.int32)
+    qd, kd, kcd, vcd = dev(q), dev(k), dev(kc), dev(vc)
+    gpu.qk_norm_rope_rows(qd, kd, dev(v), dev(qn), dev(kn), kcd, vcd, dev_i32(pos), T, hq, hkv, D,
+                          1e-6, 1e6)
+    eq, ek, ekc, evc = oracle.qk_norm_rope_rows(q, k, v, qn, kn, kc, vc, pos, hq, hkv, D, 1e-6,
+                                                1e6, oracle.GPU_ORDER)
+    assert np.array_equal(host(qd).reshape(eq.shape), eq)
+    assert np.array_equal(host(kd).reshape(ek.shape), ek)
+    assert np.array_equal(host(kcd).reshape(kc.shape), ekc)
+    assert np.array_equal(host(vcd).reshape(vc.shape), evc)
+
+
+# ---------------------------------------------------------------- attention
+
+@pytest.mark.parametrize("hq,hkv,pos", [(16, 8, 0), (16, 8, 4), (16, 8, 63), (16, 8, 64),
+                                        (16, 8, 260), (32, 8, 4095), (32, 8, 8447), (8, 8, 100),
+                                        (8, 1, 130)])
+def test_attention(gpu, oracle, hq, hkv, pos):
+    ident(f"attention {hq}/{hkv} pos{pos}")
+    rng = np.random.default_rng(hq * 10000 + pos)
+    D = 128
+    max_seq = max(pos + 1, 4096) if pos < 8000 else 8448
+    q = rand_bf16(rng, hq * D)
+    kc = rand_bf16(rng, (max_seq, hkv * D))
+    vc = rand_bf16(rng, (max_seq, hkv * D))
+    import torch
+    att = torch.zeros(gpu.attention_workspace_floats(hq, D, max_seq), dtype=torch.float32,
+                      device="cuda")
+    out = dev(np.zeros(hq * D, np.uint16))
+    scale = float(np.float32(1.0 / np.sqrt(D)))
+    gpu.attention_forward(out, dev(q), dev(kc), dev(vc), att, hq, hkv, D, dev_i32([pos]), max_seq,
+                          scale)
+    y = host(out)
+    assert np.array_equal(y, oracle.attention(q, kc, vc, hq, hkv, D, pos, scale, oracle.GPU_ORDER))
+    assert bf16_ulp_diff(y, oracle.attention(q, kc, vc, hq, hkv, D, pos, scale,
+                                             oracle.EXACT)).max() <= 2
+
+
+# ---------------------------------------------------------------- argmax
+
+def test_argmax(gpu, oracle):
+    import torch
+    ident("argmax")
+    rng = np.random.default_rng(40)
+    cases = [rand_bf16(rng, 151936) for _ in range(5)]
+    cases.append(bf16_bits(np.full(151936, 2.5)))                     # all equal -> 0
+    x = rand_bf16(rng, 151936); x[[7, 90000, 151935]] = bf16_bits(np.full(3, 50.0)); cases.append(x)
+    x = rand_bf16(rng, 151936); x[151935] = bf16_bits(np.float32(60.0)).item(); cases.append(x)
+    cases.append(bf16_bits(np.full(1000, -np.inf)))                   # all -inf -> 0
+    x = rand_bf16(rng, 5000); x[::3] = 0x7FC0; cases.append(x)        # NaNs never taken
+    cases.append(np.full(17, 0x7FC0, np.uint16))                      # all NaN -> INT_MAX
+    cases.append(rand_bf16(rng, 1))
+    cases.append(rand_bf16(rng, 13))
+    out = dev_i32([-5])
+    for x in cases:
+        gpu.argmax_forward(out, dev(x), x.size)
+        torch.cuda.synchronize()
+        assert int(out.cpu()[0]) == oracle.argmax(x)
+    # an unaligned view (falls back to 2-byte loads)
+    x = rand_bf16(rng, 1001)
+    xd = dev(x)
+    gpu.argmax_forward(out, xd[1:], 1000)
+    torch.cuda.synchronize()
+    assert int(out.cpu()[0]) == oracle.argmax(x[1:])
