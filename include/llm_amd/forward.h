@@ -103,9 +103,24 @@ typedef struct {
     int *token_out;         /* [token_capacity] tokens written by the on-device decode loop */
     int token_capacity;
     int *pos_base;          /* position of token_out[0] */
-    int *error_flag;        /* set on the device when a fed-back token is outside the vocab */
+    int *error_flag;        /* set on the device when a fed-back token is outside the vocab or a
+                               step-kernel wait timed out */
     hipGraphExec_t loop_graph; /* step + argmax + token feedback + pos advance */
+    int step_mode;          /* STEP_AUTO, STEP_GRAPH or STEP_PERSISTENT (see capture_graph) */
+    int persistent;         /* 1 once capture_graph chose the persistent step kernel */
+    void *step_ws;          /* the persistent step's barrier counters and argmax partials */
+    void *layers_dev;       /* per-layer weight pointers on the device */
+    int step_grid;          /* workgroups of the persistent step (one per CU) */
+    int next_token_valid;   /* the last forward() already computed the argmax */
+    long long *step_trace;  /* optional [5 * n_layers + 3] wall-clock stamps of the persistent
+                               step's phases (device memory, set by the caller; NULL = off) */
 } RunState;
+
+/* How capture_graph prepares the step. STEP_AUTO: the persistent step kernel (one cooperative
+ * launch per token) when the shapes have a specialisation, else a hipGraph of the per-layer
+ * kernels. STEP_GRAPH: always the hipGraph. STEP_PERSISTENT: the persistent kernel or an
+ * error. */
+enum { STEP_AUTO = 0, STEP_GRAPH = 1, STEP_PERSISTENT = 2 };
 
 /* src/loader.cu:105-139 (config.json, generation_config.json) */
 void load_config(const char *model_dir, Config *cfg);
@@ -115,7 +130,8 @@ void free_weights(Weights *w);
 /* src/loader.cu:395-419: "<name> <numel> <sum of bits> <index-weighted sum> <first value>" */
 void print_weight_checksums(const Weights *w);
 
-/* src/forward.cuh:27-34 */
+/* src/forward.cuh:27-34. capture_graph prepares the step per RunState::step_mode (set it
+ * before the call; the default is STEP_AUTO). */
 void alloc_run_state(RunState *s, const Config *cfg);
 void free_run_state(RunState *s);
 void capture_graph(const Config *cfg, const Weights *w, RunState *s);

@@ -13,13 +13,27 @@ namespace llm {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ u32x4 ld16(const void *p) { return *(const u32x4 *)p; }
+// Every buffer the library touches is device (global) memory. Pointers that the compiler
+// cannot trace to a kernel argument (fields of structs in memory) would otherwise be accessed
+// with FLAT instructions, which also count against lgkmcnt, so every later LDS or scalar wait
+// would wait for them too; the casts make them global_load/global_store.
+#define LLM_GLOBAL __attribute__((address_space(1)))
+template <class T>
+__device__ __forceinline__ LLM_GLOBAL T *gptr(T *p) {
+    return (LLM_GLOBAL T *)p;
+}
+template <class T>
+__device__ __forceinline__ const LLM_GLOBAL T *gptr(const T *p) {
+    return (const LLM_GLOBAL T *)p;
+}
+
+__device__ __forceinline__ u32x4 ld16(const void *p) { return *gptr((const u32x4 *)p); }
 // Streamed operands (weights, KV cache) are read non-temporally so they do not evict the
 // small reused vectors from L2.
 __device__ __forceinline__ u32x4 ld16_nt(const void *p) {
-    return __builtin_nontemporal_load((const u32x4 *)p);
+    return __builtin_nontemporal_load(gptr((const u32x4 *)p));
 }
-__device__ __forceinline__ void st16(void *p, u32x4 v) { *(u32x4 *)p = v; }
+__device__ __forceinline__ void st16(void *p, u32x4 v) { *gptr((u32x4 *)p) = v; }
 
 // bf16 element e of a packed 16-byte chunk (element 0 in the low half of dword 0).
 __device__ __forceinline__ float lo_f(uint32_t w) { return __uint_as_float(w << 16); }
@@ -56,20 +70,111 @@ __device__ __forceinline__ float dot8(const u32x4 &a, const u32x4 &b, float acc)
     return acc;
 }
 
+// threadIdx.x, opaque to the optimiser: lane-derived values (offsets, masks) are recomputed
+// where they are used instead of being hoisted out of long loops and held in registers.
+__device__ __forceinline__ int tid_x() {
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
+// The value of lane (lane ^ S), S a power of two below 64, without an LDS address: DPP
+// quad_perm for 1 and 2, ds_swizzle in bitmask mode (and 0x1f, xor S) for 4..16, and
+// v_permlane32_swap of the register with itself for 32 (afterwards the first result holds the
+// low half in both halves and the second the high half).
+template <int S>
+__device__ __forceinline__ int xor_lane(int x) {
+    static_assert(S > 0 && S < 64 && (S & (S - 1)) == 0, "xor distance");
+    if constexpr (S == 1) {
+        return __builtin_amdgcn_mov_dpp(x, 0xB1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
+    } else if constexpr (S == 2) {
+        return __builtin_amdgcn_mov_dpp(x, 0x4E, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
+    } else if constexpr (S < 32) {
+        return __builtin_amdgcn_ds_swizzle(x, 0x1f | (S << 10));
+    } else {
+        const auto p = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+        return (tid_x() & 32) ? (int)p[0] : (int)p[1];
+    }
+}
+template <int S>
+__device__ __forceinline__ float xor_lane(float v) {
+    return __int_as_float(xor_lane<S>(__float_as_int(v)));
+}
+
+// Steps xor S, 2S, ..., N/2 of the butterfly sum.
+template <int S, int N>
+__device__ __forceinline__ float butterfly_sum(float v) {
+    if constexpr (S < N) return butterfly_sum<2 * S, N>(v + xor_lane<S>(v));
+    else return v;
+}
+
 // Sum over aligned groups of N lanes by xor butterfly: lane l adds lane l^s for s = 1, 2, ...,
 // N/2, i.e. the balanced pairwise tree in lane order; every lane of a group ends with the sum.
 template <int N>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int s = 1; s < N; s <<= 1) v += __shfl_xor(v, s);
-    return v;
+    return butterfly_sum<1, N>(v);
 }
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
 
-__device__ __forceinline__ float wave_max(float v) {
+template <int S>
+__device__ __forceinline__ float butterfly_max(float v) {
+    if constexpr (S < 64) return butterfly_max<2 * S>(fmaxf(v, xor_lane<S>(v)));
+    else return v;
+}
+__device__ __forceinline__ float wave_max(float v) { return butterfly_max<1>(v); }
+
+// Wave sums of B rows (B a power of two up to 64) with the pairing of wave_sum, so each total
+// is bit-identical to wave_sum of that row, but scattered: at step xor 2^k for k < log2(B) a
+// lane keeps half of its rows (the upper half when bit k of its lane index is set) and adds
+// its partner's values of those rows; the remaining steps are the plain butterfly. Lane l ends
+// with the total of row scatter_row<B>(l); B - 1 + 6 - log2(B) exchanges instead of 6 B.
+template <int B>
+__device__ __forceinline__ int scatter_row(int lane) {
+    int row = 0;
 #pragma unroll
-    for (int s = 1; s < 64; s <<= 1) v = fmaxf(v, __shfl_xor(v, s));
-    return v;
+    for (int k = 0; (1 << k) < B; k++)
+        if ((lane >> k) & 1) row += B >> (k + 1);
+    return row;
+}
+template <int M, int S>
+__device__ __forceinline__ float scatter_sum_step(const float *v) {
+    if constexpr (M == 1) {
+        return butterfly_sum<S, 64>(v[0]);
+    } else {
+        const bool up = (tid_x() & S) != 0;
+        float keep[M / 2];
+#pragma unroll
+        for (int j = 0; j < M / 2; j++) {
+            const float lo = v[j], hi = v[j + M / 2];
+            const float recv = xor_lane<S>(up ? lo : hi);
+            keep[j] = (up ? hi : lo) + recv;
+        }
+        return scatter_sum_step<M / 2, 2 * S>(keep);
+    }
+}
+template <int B>
+__device__ __forceinline__ float wave_sum_scatter(const float (&v)[B]) {
+    static_assert(B >= 1 && B <= 64 && (B & (B - 1)) == 0, "rows per batch");
+    return scatter_sum_step<B, 1>(v);
+}
+
+// Larger value wins, equal values keep the lower index; NaN is never taken.
+__device__ __forceinline__ void amax_pair(float &v, int &i, float v2, int i2) {
+    if (v2 > v || (v2 == v && i2 < i)) {
+        v = v2;
+        i = i2;
+    }
+}
+
+// (max, lowest index of the max) over the wave; every lane ends with the result.
+template <int S = 1>
+__device__ __forceinline__ void wave_amax(float &v, int &i) {
+    if constexpr (S < 64) {
+        const float v2 = xor_lane<S>(v);
+        const int i2 = xor_lane<S>(i);
+        amax_pair(v, i, v2, i2);
+        wave_amax<2 * S>(v, i);
+    }
 }
 
 // 2^n for n in [-126, 127].

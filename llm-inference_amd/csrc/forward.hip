@@ -8,6 +8,7 @@
 #include "common.h"
 #include "internal.h"
 #include "llm_amd/forward.h"
+#include "step.h"
 
 using namespace llm;
 
@@ -45,7 +46,8 @@ extern "C" void alloc_run_state_seq(RunState *s, const Config *cfg, int max_seq)
               dmalloc((void **)&s->logits, (size_t)cfg->vocab_size * 2) &&
               dmalloc((void **)&s->next_token, 4) && dmalloc((void **)&s->pos, 4) &&
               dmalloc(&s->argmax_partials, (size_t)argmax_partial_count() * 8) &&
-              dmalloc((void **)&s->pos_base, 4) && dmalloc((void **)&s->error_flag, 4);
+              dmalloc((void **)&s->pos_base, 4) && dmalloc((void **)&s->error_flag, 4) &&
+              dmalloc(&s->step_ws, sizeof(StepWorkspace));
     if (!ok) return;
     HIP_OK(hipStreamCreate(&s->stream));
 }
@@ -58,7 +60,7 @@ extern "C" void free_run_state(RunState *s) {
     void *bufs[] = {s->x,  s->xb,     s->q,      s->k,      s->v,          s->attn_out,
                     s->att, s->key_cache, s->value_cache, s->hb, s->tap1, s->tap2,
                     s->logits, s->next_token, s->pos, s->argmax_partials, s->token_out,
-                    s->pos_base, s->error_flag};
+                    s->pos_base, s->error_flag, s->step_ws, s->layers_dev};
     for (void *b : bufs)
         if (b) HIP_OK(hipFree(b));
     if (s->graph) HIP_OK(hipGraphExecDestroy(s->graph));
@@ -177,12 +179,97 @@ static bool loop_body(void *p) {
     return LAUNCH_OK();
 }
 
+// The persistent step: per-layer pointers on the device, a zeroed workspace, one workgroup per
+// CU (at most the workspace's 1024 argmax slots).
+static bool prepare_persistent(const Config *cfg, const Weights *w, RunState *s) {
+    if (!s->layers_dev) {
+        if (!HIP_OK(hipMalloc(&s->layers_dev, sizeof(LayerDev) * cfg->n_layers))) return false;
+    }
+    LayerDev *host = (LayerDev *)calloc(cfg->n_layers, sizeof(LayerDev));
+    if (!host) return llm_fail("capture_graph: out of memory");
+    for (int l = 0; l < cfg->n_layers; l++) {
+        const LayerWeights *L = &w->layers[l];
+        host[l] = LayerDev{L->attn_norm, L->wq, L->wk, L->wv, L->q_norm, L->k_norm,
+                           L->wo, L->mlp_norm, L->w_gate, L->w_up, L->w_down};
+    }
+    const bool ok = HIP_OK(hipMemcpy(s->layers_dev, host, sizeof(LayerDev) * cfg->n_layers,
+                                     hipMemcpyHostToDevice)) &&
+                    HIP_OK(hipMemset(s->step_ws, 0, sizeof(StepWorkspace)));
+    free(host);
+    if (!ok) return false;
+    int grid = step_kernel_grid();
+    if (grid <= 0) return llm_fail("capture_graph: cannot read the CU count");
+    s->step_grid = grid > 1024 ? 1024 : grid;
+    s->persistent = 1;
+    return true;
+}
+
+static StepArgs step_args(const Config *cfg, const Weights *w, RunState *s, int advance) {
+    StepArgs a;
+    memset(&a, 0, sizeof a);
+    StepWorkspace *ws = (StepWorkspace *)s->step_ws;
+    a.embed = w->embed;
+    a.final_norm = w->final_norm;
+    a.lm_head = w->lm_head;
+    a.layers = (const LayerDev *)s->layers_dev;
+    a.x = s->x;
+    a.q = s->q;
+    a.k = s->k;
+    a.v = s->v;
+    a.attn_out = s->attn_out;
+    a.hb = s->hb;
+    a.logits = s->logits;
+    a.key_cache = s->key_cache;
+    a.value_cache = s->value_cache;
+    a.next_token = s->next_token;
+    a.pos = s->pos;
+    a.token_out = s->token_out;
+    a.pos_base = s->pos_base;
+    a.error_flag = s->error_flag;
+    a.bar = ws->bar;
+    a.epoch = &ws->epoch;
+    a.final_ctr = &ws->final_ctr;
+    a.amax_val = ws->amax_val;
+    a.amax_idx = ws->amax_idx;
+    a.eps = cfg->rms_norm_eps;
+    a.scale = (float)(1.0 / sqrt((double)cfg->head_dim));
+    a.n_layers = cfg->n_layers;
+    a.vocab = cfg->vocab_size;
+    a.max_seq = s->max_seq;
+    a.token_capacity = s->token_capacity;
+    a.advance = advance;
+    a.trace = s->step_trace;
+    rope_inv_freq_table(cfg->rope_theta, cfg->head_dim, a.inv_freq);
+    return a;
+}
+
+// After a synchronisation: a device-side error of the persistent step (bad token or position,
+// or a wait that timed out) is reported, and the barrier state is reset for the next use.
+static bool check_step_error(RunState *s) {
+    int err = 0;
+    if (!HIP_OK(hipMemcpy(&err, s->error_flag, 4, hipMemcpyDeviceToHost))) return false;
+    if (err == 0) return true;
+    HIP_OK(hipMemset(s->error_flag, 0, 4));
+    HIP_OK(hipMemset(s->step_ws, 0, sizeof(StepWorkspace)));
+    return llm_fail(err == 2 ? "step kernel: a grid-barrier wait timed out"
+                             : "step kernel: token or position out of range on the device");
+}
+
 // src/forward.cu:196-204
 extern "C" void capture_graph(const Config *cfg, const Weights *w, RunState *s) {
     StepCtx c{cfg, w, s};
     if (s->graph) {
         HIP_OK(hipGraphExecDestroy(s->graph));
         s->graph = nullptr;
+    }
+    s->persistent = 0;
+    if (s->step_mode != STEP_GRAPH && step_kernel_supported(cfg, s->max_seq)) {
+        prepare_persistent(cfg, w, s);
+        return;
+    }
+    if (s->step_mode == STEP_PERSISTENT) {
+        llm_fail("capture_graph: no persistent step kernel for these shapes");
+        return;
     }
     capture(s->stream, &s->graph, step_body, &c);
 }
@@ -200,19 +287,25 @@ extern "C" void forward(const Config *cfg, const Weights *w, RunState *s, int to
     if (!check_token_pos(cfg, s, token, pos)) return;
     set_token_pos_kernel<<<1, 64, 0, s->stream>>>(s->next_token, s->pos, token, pos);
     if (!LAUNCH_OK()) return;
-    if (s->graph)
+    s->next_token_valid = 0;
+    if (s->persistent) {
+        if (step_kernel_launch(cfg, step_args(cfg, w, s, 0), s->step_grid, s->stream))
+            s->next_token_valid = 1;
+    } else if (s->graph) {
         HIP_OK(hipGraphLaunch(s->graph, s->stream));
-    else
+    } else {
         forward_kernels(cfg, w, s);
+    }
 }
 
 // src/forward.cu:229-236
 extern "C" int sample_argmax(const Config *cfg, RunState *s) {
-    argmax_into_next(cfg, s);
+    if (!s->next_token_valid) argmax_into_next(cfg, s);  // the persistent step already did it
     int token = -1;
     if (!HIP_OK(hipMemcpyAsync(&token, s->next_token, 4, hipMemcpyDeviceToHost, s->stream)))
         return -1;
     if (!HIP_OK(hipStreamSynchronize(s->stream))) return -1;
+    if (s->persistent && !check_step_error(s)) return -1;
     return token;
 }
 
@@ -224,6 +317,26 @@ extern "C" int generate_greedy(const Config *cfg, const Weights *w, RunState *s,
         llm_fail("generate_greedy: %d steps from position %d pass the kv cache size %d", n_steps,
                  pos, s->max_seq);
         return -1;
+    }
+    if (s->persistent) {
+        if (s->token_capacity < n_steps) {
+            if (s->token_out) HIP_OK(hipFree(s->token_out));
+            int cap = n_steps < 256 ? 256 : n_steps;
+            if (!dmalloc((void **)&s->token_out, (size_t)cap * 4)) return -1;
+            s->token_capacity = cap;
+        }
+        set_token_pos_kernel<<<1, 64, 0, s->stream>>>(s->next_token, s->pos, token, pos);
+        set_token_pos_kernel<<<1, 64, 0, s->stream>>>(s->error_flag, s->pos_base, 0, pos);
+        if (!LAUNCH_OK()) return -1;
+        const StepArgs a = step_args(cfg, w, s, 1);
+        for (int i = 0; i < n_steps; i++)
+            if (!step_kernel_launch(cfg, a, s->step_grid, s->stream)) return -1;
+        s->next_token_valid = 1;
+        if (!HIP_OK(hipMemcpyAsync(out_tokens, s->token_out, (size_t)n_steps * 4,
+                                   hipMemcpyDeviceToHost, s->stream)) ||
+            !HIP_OK(hipStreamSynchronize(s->stream)))
+            return -1;
+        return check_step_error(s) ? 0 : -1;
     }
     if (s->token_capacity < n_steps || !s->loop_graph) {
         if (s->token_capacity < n_steps) {

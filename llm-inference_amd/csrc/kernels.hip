@@ -14,6 +14,7 @@
 
 #include "common.h"
 #include "internal.h"
+#include "rope.h"
 
 using namespace llm;
 
@@ -612,66 +613,20 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(RopeArgs a) {
     bf16 *tap = is_k ? a.k_tap : a.q_tap;
 
     float cs[NJ], sn[NJ];
-#pragma unroll
-    for (int m = 0; m < NJ; m++) {
-        const int j = lane + 64 * m;
-        cs[m] = sn[m] = 0.0f;
-        if (j < HALF) {
-            const float angle = (float)pos * a.inv_freq[j];
-            double s, c;
-            sincos_d((double)angle, &s, &c);
-            cs[m] = round_bf((float)c);
-            sn[m] = round_bf((float)s);
-        }
-    }
-
+    rope_table<D>(pos, a.inv_freq, cs, sn);
     u32x4 xa = {0, 0, 0, 0}, xb = {0, 0, 0, 0};
     if (valid) {
         xa = ld16(x + 8 * L);
         xb = ld16(x + HALF + 8 * L);
     }
     const u32x4 wa = ld16(w + 8 * L), wb = ld16(w + HALF + 8 * L);
-    float acc = dot8(xa, xa, 0.0f);
-    acc = dot8(xb, xb, acc);
-    const float total = group_sum<LH>(acc);
-    const float inv = 1.0f / sqrtf(total / (float)D + a.eps);
-    float ya[8], yb[8];
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-        ya[e] = round_bf(round_bf(elem(xa, e) * inv) * elem(wa, e));
-        yb[e] = round_bf(round_bf(elem(xb, e) * inv) * elem(wb, e));
-    }
+    u32x4 ya, yb, va, vb;
+    norm_rope<D>(xa, xb, wa, wb, a.eps, cs, sn, L, ya, yb, va, vb);
     if (valid && tap) {
-        st16(tap + off + 8 * L, u32x4{pack2(ya[0], ya[1]), pack2(ya[2], ya[3]),
-                                      pack2(ya[4], ya[5]), pack2(ya[6], ya[7])});
-        st16(tap + off + HALF + 8 * L, u32x4{pack2(yb[0], yb[1]), pack2(yb[2], yb[3]),
-                                             pack2(yb[4], yb[5]), pack2(yb[6], yb[7])});
-    }
-    float oa[8], ob[8];
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-        const int j = 8 * L + e;
-        float c = __shfl(cs[0], j & 63), s = __shfl(sn[0], j & 63);
-#pragma unroll
-        for (int m = 1; m < NJ; m++) {
-            const float cm = __shfl(cs[m], j & 63), sm = __shfl(sn[m], j & 63);
-            if ((j >> 6) == m) {
-                c = cm;
-                s = sm;
-            }
-        }
-        const float a_cos = round_bf(ya[e] * c);
-        const float b_sin = round_bf(yb[e] * s);
-        const float b_cos = round_bf(yb[e] * c);
-        const float a_sin = round_bf(ya[e] * s);
-        oa[e] = a_cos - b_sin;
-        ob[e] = b_cos + a_sin;
+        st16(tap + off + 8 * L, ya);
+        st16(tap + off + HALF + 8 * L, yb);
     }
     if (valid) {
-        const u32x4 va = {pack2(oa[0], oa[1]), pack2(oa[2], oa[3]), pack2(oa[4], oa[5]),
-                          pack2(oa[6], oa[7])};
-        const u32x4 vb = {pack2(ob[0], ob[1]), pack2(ob[2], ob[3]), pack2(ob[4], ob[5]),
-                          pack2(ob[6], ob[7])};
         st16(x + 8 * L, va);
         st16(x + HALF + 8 * L, vb);
         if (is_k) {
@@ -683,7 +638,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(RopeArgs a) {
 
 // inv_freq_j = 1 / fp32(pow(theta, fp32(2j / D))) as HF computes it (modeling_qwen3.py:121),
 // cached per (theta, D).
-static void rope_inv_freq(float theta, int D, float *out) {
+void rope_inv_freq_table(float theta, int D, float *out) {
     static std::mutex mu;
     static float cached_theta = -1.0f;
     static int cached_d = -1;
@@ -740,7 +695,7 @@ static void launch_qk_norm_rope(bf16 *q, bf16 *k, const bf16 *v, const bf16 *q_n
     a.qg = (n_heads + hpw - 1) / hpw;
     a.kg = (n_kv_heads + hpw - 1) / hpw;
     a.vg = a.kg;
-    rope_inv_freq(theta, head_dim, a.inv_freq);
+    rope_inv_freq_table(theta, head_dim, a.inv_freq);
     const long waves = (long)n_tokens * (a.qg + a.kg + a.vg);
     const unsigned blocks = (unsigned)((waves + 3) / 4);
     if (head_dim == 64)
@@ -913,9 +868,7 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnArgs a) {
 #pragma unroll
         for (int r = 0; r < REP; r++)
 #pragma unroll
-            for (int e = 0; e < 8; e++)
-#pragma unroll
-                for (int s = LP; s < 64; s <<= 1) acc[r][e] += __shfl_xor(acc[r][e], s);
+            for (int e = 0; e < 8; e++) acc[r][e] = butterfly_sum<LP, 64>(acc[r][e]);
         if (G == 0)
 #pragma unroll
             for (int r = 0; r < REP; r++)
@@ -1015,21 +968,8 @@ constexpr int AMAX_GROUPS = 256;
 __device__ float g_amax_val[AMAX_GROUPS];
 __device__ int g_amax_idx[AMAX_GROUPS];
 
-// Larger value wins, equal values keep the lower index; NaN is never taken.
-__device__ __forceinline__ void amax_pair(float &v, int &i, float v2, int i2) {
-    if (v2 > v || (v2 == v && i2 < i)) {
-        v = v2;
-        i = i2;
-    }
-}
-
 __device__ __forceinline__ void block_amax(float &v, int &i, float *lv, int *li) {
-#pragma unroll
-    for (int s = 1; s < 64; s <<= 1) {
-        const float v2 = __shfl_xor(v, s);
-        const int i2 = __shfl_xor(i, s);
-        amax_pair(v, i, v2, i2);
-    }
+    wave_amax(v, i);
     const int w = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0) {
         lv[w] = v;

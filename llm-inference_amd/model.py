@@ -49,7 +49,12 @@ class RunState(ctypes.Structure):
                 ("hb", _vp), ("tap1", _vp), ("tap2", _vp), ("logits", _vp),
                 ("next_token", _vp), ("pos", _vp), ("stream", _vp), ("graph", _vp),
                 ("argmax_partials", _vp), ("token_out", _vp), ("token_capacity", _i),
-                ("pos_base", _vp), ("error_flag", _vp), ("loop_graph", _vp)]
+                ("pos_base", _vp), ("error_flag", _vp), ("loop_graph", _vp), ("step_mode", _i),
+                ("persistent", _i), ("step_ws", _vp), ("layers_dev", _vp), ("step_grid", _i),
+                ("next_token_valid", _i), ("step_trace", ctypes.POINTER(ctypes.c_longlong))]
+
+
+STEP_MODES = {"auto": 0, "graph": 1, "persistent": 2}
 
 
 _PC, _PW, _PS = ctypes.POINTER(Config), ctypes.POINTER(Weights), ctypes.POINTER(RunState)
@@ -151,6 +156,16 @@ def copy_to_host(ptr, nbytes, out=None):
     return out
 
 
+def copy_to_device(ptr, arr):
+    """Synchronous host-to-device copy of a contiguous numpy array to device address ptr."""
+    import numpy as np
+    arr = np.ascontiguousarray(arr)
+    rt = _hip()
+    rc = rt.hipMemcpy(ptr, arr.ctypes.data, arr.nbytes, 1)  # hipMemcpyHostToDevice
+    if rc != 0:
+        raise LlmError(f"hipMemcpy host-to-device failed ({rc})")
+
+
 def weight_bytes_per_step(cfg):
     return lib().weight_bytes_per_step(ctypes.byref(cfg))
 
@@ -165,9 +180,10 @@ class Decoder:
     weights: ("synth", seed, std, gamma_std) for seeded random init, or a model directory.
     """
 
-    def __init__(self, cfg, weights=("synth", 0, 0.02, 0.1), max_seq=None):
+    def __init__(self, cfg, weights=("synth", 0, 0.02, 0.1), max_seq=None, mode="auto"):
         L = lib()
         self.cfg = cfg
+        self.mode = mode
         self.w = Weights()
         self.s = RunState()
         self._w_ok = self._s_ok = False
@@ -203,9 +219,16 @@ class Decoder:
     def stream(self):
         return self.s.stream
 
-    def capture_graph(self):
+    def capture_graph(self, mode=None):
+        """Prepares the replayed step: the persistent step kernel ("auto" when the shapes have
+        a specialisation, or "persistent") or a hipGraph of the per-layer kernels ("graph")."""
+        self.s.step_mode = STEP_MODES[mode or self.mode]
         lib().capture_graph(ctypes.byref(self.cfg), ctypes.byref(self.w), ctypes.byref(self.s))
         check()
+
+    @property
+    def persistent(self):
+        return bool(self.s.persistent)
 
     def forward(self, token, pos):
         lib().forward(ctypes.byref(self.cfg), ctypes.byref(self.w), ctypes.byref(self.s), token,
@@ -275,6 +298,11 @@ class Decoder:
         copy_to_host(self.s.key_cache, k.nbytes, k)
         copy_to_host(self.s.value_cache, v.nbytes, v)
         return k, v
+
+    def set_kv_cache(self, k, v):
+        """Overwrites the device KV caches with uint16 arrays [n_layers, max_seq, kv_dim]."""
+        copy_to_device(self.s.key_cache, k)
+        copy_to_device(self.s.value_cache, v)
 
     def weight_bytes_per_step(self):
         return weight_bytes_per_step(self.cfg)

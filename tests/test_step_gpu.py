@@ -185,13 +185,16 @@ def _prompt(seed=0):
     return [int(t) for t in np.random.default_rng(seed).integers(0, 151936, 5)]
 
 
-def test_qwen3_06b_greedy_32_bit_exact(qwen06b, oracle):
+@pytest.mark.parametrize("mode", ["graph", "persistent"])
+def test_qwen3_06b_greedy_32_bit_exact(qwen06b, oracle, mode):
     """Qwen3-0.6B shapes, seeded N(0, 0.02) weights: 5-token prompt + 32 greedy tokens, GPU
-    (graph-replayed on-device loop) == oracle GPU-order, token for token."""
-    ident("0.6B greedy 32")
+    (hipGraph of the per-layer kernels, or the persistent step kernel; both replayed on the
+    device) == oracle GPU-order, token for token."""
+    ident(f"0.6B greedy 32 {mode}")
     dec, w = qwen06b
     prompt = _prompt()
-    dec.capture_graph()
+    dec.capture_graph(mode)
+    assert dec.persistent == (mode == "persistent")
     for pos, tok in enumerate(prompt):
         dec.forward(tok, pos)
     first = dec.sample_argmax()
@@ -212,6 +215,7 @@ def test_qwen3_06b_greedy_256_vs_exact_oracle(qwen06b, oracle):
     ref/greedy.py:14-31)."""
     ident("0.6B greedy 256")
     dec, w = qwen06b
+    dec.capture_graph("persistent")
     prompt = _prompt(1)
     for pos, tok in enumerate(prompt):
         dec.forward(tok, pos)
@@ -236,3 +240,67 @@ def test_qwen3_06b_greedy_256_vs_exact_oracle(qwen06b, oracle):
     flips = [(i, gaps[i]) for i in range(256) if exact[i] != got[i]]
     print(f"teacher-forced agreement with exact arithmetic: {256 - len(flips)}/256, flips {flips}")
     assert all(g <= TIE_GAP for _, g in flips), flips
+
+
+def test_persistent_step_logits_per_position(gpu, oracle):
+    """The persistent step on the smallest specialised shapes (hidden 512, 8/4 heads,
+    intermediate 1024): logits and the fused argmax bit-identical to the oracle at every
+    position, and identical to the hipGraph step."""
+    ident("persistent step small shapes")
+    from llm_inference_amd import model
+    cfg = model.make_config(hidden_size=512, intermediate_size=1024, n_layers=3, n_heads=8,
+                            n_kv_heads=4, vocab_size=5000, max_seq_len=200)
+    dec = model.Decoder(cfg, ("synth", 3, 0.02, 0.1))
+    try:
+        w = dec.host_weights()
+        orc = oracle.Model(oracle_cfg(cfg), w, max_seq=200)
+        tokens = [int(t) for t in np.random.default_rng(5).integers(0, 5000, 150)]
+        dec.capture_graph("persistent")
+        per = []
+        for pos, tok in enumerate(tokens):
+            dec.forward(tok, pos)
+            nxt = dec.sample_argmax()
+            ref = orc.forward(tok, pos, oracle.GPU_ORDER)
+            assert np.array_equal(dec.logits(), orc.logits), pos
+            assert nxt == ref, pos
+            per.append(dec.logits())
+        dec.capture_graph("graph")
+        for pos, tok in enumerate(tokens[:70]):
+            dec.forward(tok, pos)
+            dec.sample_argmax()
+            assert np.array_equal(dec.logits(), per[pos]), pos
+    finally:
+        dec.close()
+
+
+def test_persistent_step_long_context(qwen06b, oracle):
+    """One decode position at 5000 with the KV cache below it filled with N(0, 1): the
+    persistent step's attention over 79 blocks of 64 positions is bit-identical to the
+    oracle's."""
+    ident("persistent step pos 5000")
+    from llm_inference_amd import model
+    dec0, w = qwen06b
+    cfg = model.qwen3_config("0.6B", max_seq_len=5008)
+    dec = model.Decoder(cfg, ("synth", 0, 0.02, 0.1))
+    try:
+        rng = np.random.default_rng(7)
+        kvd = cfg.n_kv_heads * cfg.head_dim
+        k = rand_bf16(rng, (cfg.n_layers, 5008, kvd))
+        v = rand_bf16(rng, (cfg.n_layers, 5008, kvd))
+        dec.set_kv_cache(k, v)
+        orc = oracle.Model(oracle_cfg(cfg), w, max_seq=5008)
+        orc.bufs["key_cache"][:] = k.reshape(-1)
+        orc.bufs["value_cache"][:] = v.reshape(-1)
+        dec.capture_graph("persistent")
+        dec.forward(1234, 5000)
+        nxt = dec.sample_argmax()
+        ref = orc.forward(1234, 5000, oracle.GPU_ORDER)
+        assert np.array_equal(dec.logits(), orc.logits)
+        assert nxt == ref
+        kk, vv = dec.kv_cache()
+        assert np.array_equal(kk[:, 5000].reshape(-1),
+                              orc.bufs["key_cache"].reshape(k.shape)[:, 5000].reshape(-1))
+        assert np.array_equal(vv[:, 5000].reshape(-1),
+                              orc.bufs["value_cache"].reshape(v.shape)[:, 5000].reshape(-1))
+    finally:
+        dec.close()
