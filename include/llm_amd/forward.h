@@ -108,12 +108,17 @@ typedef struct {
     hipGraphExec_t loop_graph; /* step + argmax + token feedback + pos advance */
     int step_mode;          /* STEP_AUTO, STEP_GRAPH or STEP_PERSISTENT (see capture_graph) */
     int persistent;         /* 1 once capture_graph chose the persistent step kernel */
-    void *step_ws;          /* the persistent step's barrier counters and argmax partials */
+    void *step_ws;          /* the persistent step's sequence counter, argmax partials and
+                               tagged activation vectors */
     void *layers_dev;       /* per-layer weight pointers on the device */
     int step_grid;          /* workgroups of the persistent step (one per CU) */
     int next_token_valid;   /* the last forward() already computed the argmax */
-    long long *step_trace;  /* optional [5 * n_layers + 3] wall-clock stamps of the persistent
-                               step's phases (device memory, set by the caller; NULL = off) */
+    long long *step_trace;  /* optional [4 * n_layers + 3 + 8 * step_grid] wall-clock stamps
+                               (device memory, set by the caller; NULL = off): [0] start, then
+                               per layer the moments the first matrix workgroup has its inputs
+                               for the q/k/v, o, gate/up and down rows, then for the LM head,
+                               and the end; then, for layer 1 and every workgroup, 8 stamps:
+                               input staged / results stored for each of its 4 phases */
 } RunState;
 
 /* How capture_graph prepares the step. STEP_AUTO: the persistent step kernel (one cooperative

@@ -47,7 +47,7 @@ extern "C" void alloc_run_state_seq(RunState *s, const Config *cfg, int max_seq)
               dmalloc((void **)&s->next_token, 4) && dmalloc((void **)&s->pos, 4) &&
               dmalloc(&s->argmax_partials, (size_t)argmax_partial_count() * 8) &&
               dmalloc((void **)&s->pos_base, 4) && dmalloc((void **)&s->error_flag, 4) &&
-              dmalloc(&s->step_ws, sizeof(StepWorkspace));
+              dmalloc(&s->step_ws, step_workspace_bytes(cfg));
     if (!ok) return;
     HIP_OK(hipStreamCreate(&s->stream));
 }
@@ -194,7 +194,7 @@ static bool prepare_persistent(const Config *cfg, const Weights *w, RunState *s)
     }
     const bool ok = HIP_OK(hipMemcpy(s->layers_dev, host, sizeof(LayerDev) * cfg->n_layers,
                                      hipMemcpyHostToDevice)) &&
-                    HIP_OK(hipMemset(s->step_ws, 0, sizeof(StepWorkspace)));
+                    HIP_OK(hipMemset(s->step_ws, 0, step_workspace_bytes(cfg)));
     free(host);
     if (!ok) return false;
     int grid = step_kernel_grid();
@@ -212,12 +212,6 @@ static StepArgs step_args(const Config *cfg, const Weights *w, RunState *s, int 
     a.final_norm = w->final_norm;
     a.lm_head = w->lm_head;
     a.layers = (const LayerDev *)s->layers_dev;
-    a.x = s->x;
-    a.q = s->q;
-    a.k = s->k;
-    a.v = s->v;
-    a.attn_out = s->attn_out;
-    a.hb = s->hb;
     a.logits = s->logits;
     a.key_cache = s->key_cache;
     a.value_cache = s->value_cache;
@@ -226,7 +220,12 @@ static StepArgs step_args(const Config *cfg, const Weights *w, RunState *s, int 
     a.token_out = s->token_out;
     a.pos_base = s->pos_base;
     a.error_flag = s->error_flag;
-    a.bar = ws->bar;
+    uint32_t *tagged = (uint32_t *)(ws + 1);
+    const int qd = cfg->n_heads * cfg->head_dim, kvd = cfg->n_kv_heads * cfg->head_dim;
+    a.tx = tagged;
+    a.tqkv = a.tx + STEP_REPLICAS * step_replica_stride(cfg->hidden_size);
+    a.tattn = a.tqkv + step_replica_stride(qd + 2 * kvd);
+    a.thb = a.tattn + STEP_REPLICAS * step_replica_stride(qd);
     a.epoch = &ws->epoch;
     a.final_ctr = &ws->final_ctr;
     a.amax_val = ws->amax_val;
@@ -244,14 +243,15 @@ static StepArgs step_args(const Config *cfg, const Weights *w, RunState *s, int 
 }
 
 // After a synchronisation: a device-side error of the persistent step (bad token or position,
-// or a wait that timed out) is reported, and the barrier state is reset for the next use.
-static bool check_step_error(RunState *s) {
+// or a wait that timed out) is reported, and the workspace (sequence counter and tagged
+// vectors) is zeroed for the next use.
+static bool check_step_error(const Config *cfg, RunState *s) {
     int err = 0;
     if (!HIP_OK(hipMemcpy(&err, s->error_flag, 4, hipMemcpyDeviceToHost))) return false;
     if (err == 0) return true;
     HIP_OK(hipMemset(s->error_flag, 0, 4));
-    HIP_OK(hipMemset(s->step_ws, 0, sizeof(StepWorkspace)));
-    return llm_fail(err == 2 ? "step kernel: a grid-barrier wait timed out"
+    HIP_OK(hipMemset(s->step_ws, 0, step_workspace_bytes(cfg)));
+    return llm_fail(err == 2 ? "step kernel: a wait for another workgroup's data timed out"
                              : "step kernel: token or position out of range on the device");
 }
 
@@ -305,7 +305,7 @@ extern "C" int sample_argmax(const Config *cfg, RunState *s) {
     if (!HIP_OK(hipMemcpyAsync(&token, s->next_token, 4, hipMemcpyDeviceToHost, s->stream)))
         return -1;
     if (!HIP_OK(hipStreamSynchronize(s->stream))) return -1;
-    if (s->persistent && !check_step_error(s)) return -1;
+    if (s->persistent && !check_step_error(cfg, s)) return -1;
     return token;
 }
 
@@ -336,7 +336,7 @@ extern "C" int generate_greedy(const Config *cfg, const Weights *w, RunState *s,
                                    hipMemcpyDeviceToHost, s->stream)) ||
             !HIP_OK(hipStreamSynchronize(s->stream)))
             return -1;
-        return check_step_error(s) ? 0 : -1;
+        return check_step_error(cfg, s) ? 0 : -1;
     }
     if (s->token_capacity < n_steps || !s->loop_graph) {
         if (s->token_capacity < n_steps) {

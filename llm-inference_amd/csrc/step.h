@@ -9,32 +9,43 @@ struct LayerDev {
         *w_down;
 };
 
+// Tagged vectors: element i of a bf16 activation vector travels between workgroups as the
+// 32-bit word (bf16 bits << 16) | tag, where tag (1..65535) names the phase that wrote it.
+// A consumer polls the words it needs until every tag is the expected one; there is no grid
+// barrier. tx: residual stream [H], tqkv: q|k|v [QD + 2 KVD], tattn: attention output [QD],
+// thb: SwiGLU output [I]. The vectors read by many workgroups (tx, tattn, thb) are written in
+// STEP_REPLICAS copies, step_replica_stride(n) words apart, and workgroup b reads copy
+// b % STEP_REPLICAS: fewer pollers per cache line make a written value visible sooner.
+constexpr int STEP_REPLICAS = 8;
+constexpr size_t step_replica_stride(size_t n) { return (n + 1023) / 1024 * 1024; }
+
 struct StepArgs {
     const bf16 *embed, *final_norm, *lm_head;
     const LayerDev *layers;
-    bf16 *x, *q, *k, *v, *attn_out, *hb, *logits, *key_cache, *value_cache;
+    bf16 *logits, *key_cache, *value_cache;
+    uint32_t *tx, *tqkv, *tattn, *thb;
     int *next_token, *pos, *token_out, *pos_base, *error_flag;
-    unsigned *bar;        // grid-barrier counters, 16 lines of 128 bytes
-    unsigned *epoch;      // barriers completed so far (the counters' expected base)
+    unsigned *epoch;      // phases completed over all launches (the tag base)
     unsigned *final_ctr;  // workgroups done with the LM head
     float *amax_val;      // per-workgroup argmax partials
     int *amax_idx;
-    long long *trace;     // optional: wall-clock stamp after every barrier (workgroup 0)
+    long long *trace;     // optional wall-clock stamps of one workgroup's phases
     float eps, scale;
     int n_layers, vocab, max_seq, token_capacity, advance;
     float inv_freq[64];
 };
 
-// Workspace the step kernel keeps in RunState::step_ws (zeroed at allocation).
+// Workspace the step kernel keeps in RunState::step_ws (zeroed at allocation and after an
+// error; a zero tag never matches), followed by the tagged vectors.
 struct StepWorkspace {
-    unsigned bar[16 * 32];
     unsigned epoch;
     unsigned final_ctr;
-    unsigned pad[30];
+    unsigned pad[62];
     float amax_val[1024];
     int amax_idx[1024];
 };
 
+size_t step_workspace_bytes(const Config *cfg);
 bool step_kernel_supported(const Config *cfg, int max_seq);
 int step_kernel_grid();
 bool step_kernel_launch(const Config *cfg, const StepArgs &args, int grid, hipStream_t stream);

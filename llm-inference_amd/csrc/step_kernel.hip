@@ -1,7 +1,8 @@
 // The whole decode step as one persistent kernel for gfx950: one workgroup of 8 waves per CU,
-// cooperatively launched, phases separated by grid barriers. Each phase computes exactly what
-// the standalone kernels compute (same per-row, per-head and per-block arithmetic), so the
-// step is bit-identical to the multi-kernel step it replaces (src/forward.cu:118-193 order):
+// cooperatively launched (so all workgroups are resident), with no grid barrier. Each phase
+// computes exactly what the standalone kernels compute (same per-row, per-head and per-block
+// arithmetic), so the step is bit-identical to the multi-kernel step it replaces
+// (src/forward.cu:118-193 order):
 //
 //   per layer:  rmsnorm + q/k/v rows | QK-norm + RoPE + KV write + attention, one workgroup
 //               per query head | o rows + residual | rmsnorm + gate/up rows + SwiGLU |
@@ -9,13 +10,16 @@
 //   final:      rmsnorm + LM-head rows + per-workgroup argmax; the last workgroup to finish
 //               reduces the argmax, records the token and advances the position
 //
-// Activations cross workgroups (and XCDs, whose L2s are not coherent) only through
-// agent-scope atomic loads/stores (global_load/store ... sc1); weights and the KV history are
-// read with plain non-temporal loads. A grid barrier is: every thread waits for its own
-// stores (s_waitcnt), the workgroup syncs, thread 0 adds to one of 16 counters (one per
-// 128-byte line), and wave 0 polls the 16 counters until each has its expected count. Every
-// wait is bounded: on timeout the step sets an error flag and all later waits fall through, so
-// the grid always drains.
+// Activations cross workgroups (and XCDs, whose L2s are not coherent) as tagged vectors:
+// element i is the 32-bit word (bf16 bits << 16) | tag, stored and loaded with agent-scope
+// atomics (global_store/load ... sc1). The tag names the phase that wrote the value, so a
+// consumer workgroup polls exactly the words it needs until every tag is the expected one,
+// copying them into LDS; the data is its own ready signal and no phase waits for a barrier,
+// for its stores to complete, or for workgroups it does not depend on. A writer of a vector's
+// next version always depends (through the phases between) on every reader of its previous
+// version, so no value is overwritten before it has been read. Weights and the KV history are
+// read with plain non-temporal loads, requested a phase or more ahead. Every wait is bounded:
+// on timeout the step sets an error flag and later waits give up at once, so the grid drains.
 #include <limits.h>
 #include <string.h>
 
@@ -28,34 +32,21 @@ using namespace llm;
 
 namespace {
 
-constexpr int WAVES = 8;                 // waves per workgroup
+constexpr int WAVES = 8;                   // waves per workgroup
 constexpr int THREADS = 64 * WAVES;
-constexpr int BAR_GROUPS = 16;           // barrier counter lines
 constexpr long long SPIN_LIMIT = 1 << 22;  // polls before a wait gives up (~ seconds)
+constexpr int PHASES = 5;                  // tagged vectors written per layer
 
 // ---------------------------------------------------------------- coherent access
 
 __device__ __forceinline__ uint64_t ld_coh64(const void *p) {
     return __hip_atomic_load(gptr((uint64_t *)p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void st_coh64(void *p, uint64_t v) {
-    __hip_atomic_store(gptr((uint64_t *)p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ u32x4 ld_coh16(const void *p) {
-    const uint64_t a = ld_coh64(p), b = ld_coh64((const char *)p + 8);
-    return u32x4{(uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32)};
-}
-__device__ __forceinline__ void st_coh_bf16(bf16 *p, uint32_t v) {
-    __hip_atomic_store(gptr((unsigned short *)p), (unsigned short)v, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint32_t ld_coh_bf16(const bf16 *p) {
-    return __hip_atomic_load(gptr((unsigned short *)p), __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-}
 __device__ __forceinline__ unsigned ld_coh_u32(const unsigned *p) {
     return __hip_atomic_load(gptr((unsigned *)p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+
+// ---------------------------------------------------------------- arguments
 
 typedef const __attribute__((address_space(4))) StepArgs KArgs;
 typedef const __attribute__((address_space(4))) LayerDev KLayer;
@@ -89,88 +80,109 @@ __device__ __forceinline__ KLayer &klayer(KArgs &a, int l) {
     return *t;
 }
 
-// ---------------------------------------------------------------- grid barrier
+// ---------------------------------------------------------------- tagged vectors
 
-struct Barrier {
-    unsigned epoch;  // barriers completed since the counters were zero
-    int n;           // barriers passed in this launch
+// Tag of the seq-th tagged phase since the workspace was zeroed: 1..65535, never 0 (the
+// zeroed state). A word is rewritten every layer, so values 65535 phases apart never meet.
+__device__ __forceinline__ uint32_t tag_of(unsigned seq) { return 1u + seq % 65535u; }
 
-    __device__ __forceinline__ void init(unsigned base) {
-        epoch = base;
-        n = 0;
-        stamp();
-    }
+__device__ __forceinline__ void put_tagged(uint32_t *v, int i, uint32_t bits, uint32_t tag) {
+    __hip_atomic_store(gptr(v + i), (bits << 16) | tag, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
 
-    // optional wall-clock stamps (workgroup 0, thread 0)
-    __device__ __forceinline__ void stamp() {
-        if (blockIdx.x == 0 && threadIdx.x == 0) {
-            long long *trace = kargs().trace;
-            if (trace) gptr(trace)[n] = wall_clock64();
-        }
-    }
+// Element i of a replicated tagged vector of n elements, into every copy.
+template <int N>
+__device__ __forceinline__ void put_tagged_all(uint32_t *v, int i, uint32_t bits, uint32_t tag) {
+    constexpr int STRIDE = (int)step_replica_stride(N);
+#pragma unroll
+    for (int q = 0; q < STEP_REPLICAS; q++) put_tagged(v + q * STRIDE, i, bits, tag);
+}
 
-    // Arrival: this thread's coherent stores are complete (s_waitcnt), the workgroup has
-    // synced, and thread 0 adds to its counter line. Loads issued between arrive() and wait()
-    // (the next phase's weights) overlap the wait.
-    __device__ __forceinline__ void arrive() {
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        epoch++;
-        if (threadIdx.x == 0)
-            __hip_atomic_fetch_add(gptr(&kargs().bar[(blockIdx.x % BAR_GROUPS) * 32]), 1u,
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+// The copy of a replicated tagged vector of n elements that this workgroup reads.
+template <int N>
+__device__ __forceinline__ const uint32_t *my_copy(const uint32_t *v) {
+    return v + (blockIdx.x % STEP_REPLICAS) * (int)step_replica_stride(N);
+}
 
-    // Wave 0 polls the counter lines until each holds epoch x its member count.
-    __device__ __forceinline__ void wait() {
-        if (threadIdx.x < 64) {
-            unsigned *ctr = kargs().bar;
-            int *err = kargs().error_flag;
-            const int g = threadIdx.x;
-            // workgroups b with b % BAR_GROUPS == g
-            const unsigned members = (unsigned)(((int)gridDim.x - g + BAR_GROUPS - 1) / BAR_GROUPS);
-            const unsigned need = g < BAR_GROUPS ? epoch * members : 0u;
-            long long spins = 0;
-            for (;;) {
-                const unsigned c = g < BAR_GROUPS
-                                       ? __hip_atomic_load(gptr(&ctr[g * 32]), __ATOMIC_RELAXED,
-                                                           __HIP_MEMORY_SCOPE_AGENT)
-                                       : 0u;
-                if (__all((int)(c - need) >= 0)) break;
-                if (++spins > SPIN_LIMIT ||
-                    __hip_atomic_load(gptr(err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
-                    if (threadIdx.x == 0)
-                        __hip_atomic_store(gptr(err), 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    break;
-                }
+// Polls the 64-bit words src(p) (two tagged elements each) for the pairs p = threadIdx.x +
+// THREADS*j < PAIRS until both tags equal `tag`, and writes the bf16 pairs to dst[p] (LDS). The
+// whole workgroup takes part; it syncs before (the previous contents of dst have been read)
+// and after. Bounded: on timeout, or once another wave has timed out, it sets the error flag
+// and goes on with what it read.
+template <int PAIRS, class Src>
+__device__ __forceinline__ void stage_pairs(Src src, uint32_t tag, uint32_t *dst, int *err) {
+    constexpr int P = (PAIRS + THREADS - 1) / THREADS;
+    __syncthreads();
+    const int t0 = threadIdx.x;
+    uint64_t w[P];
+    long long spins = 0;
+    for (;;) {
+        bool fresh = true;
+#pragma unroll
+        for (int j = 0; j < P; j++) {
+            const int p = t0 + THREADS * j;
+            if (p < PAIRS) {
+                w[j] = ld_coh64(src(p));
+                fresh &= (uint32_t)(w[j] & 0xffffu) == tag &&
+                         (uint32_t)((w[j] >> 32) & 0xffffu) == tag;
             }
         }
-        __syncthreads();
-        n++;
-        stamp();
+        if (fresh) break;
+        if ((++spins & 63) == 0 && (spins > SPIN_LIMIT || ld_coh_u32((const unsigned *)err))) {
+            __hip_atomic_store(gptr(err), 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
     }
+#pragma unroll
+    for (int j = 0; j < P; j++) {
+        const int p = t0 + THREADS * j;
+        if (p < PAIRS)
+            dst[p] = (uint32_t)((w[j] >> 16) & 0xffffu) | ((uint32_t)(w[j] >> 48) << 16);
+    }
+    __syncthreads();
+}
 
-    __device__ __forceinline__ void sync() {
-        arrive();
-        wait();
-    }
-};
+// Elements [0, N) of tagged vector v into LDS as plain bf16 (N even).
+template <int N>
+__device__ __forceinline__ void stage_vector(const uint32_t *v, uint32_t tag, uint32_t *dst,
+                                             int *err) {
+    stage_pairs<N / 2>([=](int p) { return v + 2 * p; }, tag, dst, err);
+}
+
+// The embedding row as the first layer's input (read-only: nothing to wait for).
+template <int N>
+__device__ __forceinline__ void stage_plain(const bf16 *row, uint32_t *dst) {
+    __syncthreads();
+    for (int c = threadIdx.x; c < N / 8; c += THREADS) ((u32x4 *)dst)[c] = ld16(row + 8 * c);
+    __syncthreads();
+}
 
 // ---------------------------------------------------------------- wave building blocks
 
-// The input vector of a GEMV as this lane's chunks: chunk lane + 64k of the vector.
+// The input vector of a GEMV as this lane's chunks (chunk lane + 64k), from LDS.
 template <int NC>
-__device__ __forceinline__ void load_vec_coh(const bf16 *v, u32x4 (&out)[NC]) {
+__device__ __forceinline__ void lds_chunks(const uint32_t *vec, u32x4 (&out)[NC]) {
     const int lane = tid_x() & 63;
 #pragma unroll
-    for (int k = 0; k < NC; k++) out[k] = ld_coh16(v + 8 * (lane + 64 * k));
+    for (int k = 0; k < NC; k++) out[k] = ((const u32x4 *)vec)[lane + 64 * k];
 }
 
-// RMSNorm of a row of 512*NC elements held as chunks (rmsnorm_wave_kernel arithmetic).
+// This lane's chunks (lane + 64k) of a vector in global memory (norm weights: plain loads, so
+// they stay cached from one step to the next).
 template <int NC>
-__device__ __forceinline__ void wave_rmsnorm(const u32x4 (&x)[NC], const bf16 *w, float eps,
-                                             u32x4 (&out)[NC]) {
+__device__ __forceinline__ void load_chunks(const bf16 *v, u32x4 (&out)[NC]) {
     const int lane = tid_x() & 63;
+#pragma unroll
+    for (int k = 0; k < NC; k++) out[k] = ld16(v + 8 * (lane + 64 * k));
+}
+
+// RMSNorm of a row of 512*NC elements held as chunks, with the weight chunks wn
+// (rmsnorm_wave_kernel arithmetic).
+template <int NC>
+__device__ __forceinline__ void wave_rmsnorm(const u32x4 (&x)[NC], const u32x4 (&wn)[NC],
+                                             float eps, u32x4 (&out)[NC]) {
     float acc = 0.0f;
 #pragma unroll
     for (int k = 0; k < NC; k++) acc = dot8(x[k], x[k], acc);
@@ -178,7 +190,7 @@ __device__ __forceinline__ void wave_rmsnorm(const u32x4 (&x)[NC], const bf16 *w
     const float inv = 1.0f / sqrtf(total / (float)(512 * NC) + eps);
 #pragma unroll
     for (int k = 0; k < NC; k++) {
-        const u32x4 wv = ld16(w + 8 * (lane + 64 * k));
+        const u32x4 wv = wn[k];
         float r[8];
 #pragma unroll
         for (int e = 0; e < 8; e++) r[e] = round_bf(elem(x[k], e) * inv) * elem(wv, e);
@@ -203,48 +215,59 @@ struct Rows {
     }
 };
 
-// Rows [r0, r1) against xin, B rows per batch, the first batch already in `batch` (loaded
-// before the barrier that precedes this phase); epi(row, sum) runs in one of lanes 0..B-1
-// (gemv_kernel arithmetic: per-lane fma over the chunks in order, then the wave tree).
-template <int NC, int B, class RowP, class Epi>
+// The B row sums of a batch against xin (gemv_kernel arithmetic: per-lane fma over the chunks
+// in order, then the wave tree); lane l gets row scatter_row<B>(l) of the batch.
+template <int NC, int B>
+__device__ __forceinline__ float batch_sums(const Rows<NC, B> &b, const u32x4 (&xin)[NC]) {
+    float part[B];
+#pragma unroll
+    for (int i = 0; i < B; i++) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NC; k++) acc = dot8(b.w[i][k], xin[k], acc);
+        part[i] = acc;
+    }
+    return wave_sum_scatter<B>(part);
+}
+
+// Rows [r0, r1) against xin, B rows per batch, the first batch already in `cur` (requested a
+// phase ahead). With STREAM the next batch is requested before the current one is reduced
+// (two batches in flight), else after. epi(row, sum, v) runs in one of lanes 0..B-1 and
+// returns bf16 bits; v is `own` of lane row - r0. `own` is a per-row value the wave keeps
+// (lane j: row r0 + j, at most 64 rows): with KEEP it is replaced by epi's result for the row,
+// so a wave carries the residual rows it updates from one phase to the next. Lane
+// scatter_row<B>(k) computes batch row k, and scatter_row<B> is its own inverse.
+template <int NC, int B, bool STREAM, bool KEEP = false, class RowP, class Epi>
 __device__ __forceinline__ void wave_gemv(RowP rowp, int r0, int r1, const u32x4 (&xin)[NC],
-                                          Rows<NC, B> &batch, Epi epi, uint32_t lane_val = 0) {
+                                          Rows<NC, B> &cur, Epi epi, uint32_t *own = nullptr) {
     const int lane = tid_x() & 63;
-    for (int r = r0; r < r1; r += B) {
-        if (r != r0) batch.load(rowp, r, r1);
-        float part[B];
-#pragma unroll
-        for (int i = 0; i < B; i++) {
-            float acc = 0.0f;
-#pragma unroll
-            for (int k = 0; k < NC; k++) acc = dot8(batch.w[i][k], xin[k], acc);
-            part[i] = acc;
-        }
-        const float t = wave_sum_scatter<B>(part);
+    auto finish = [&](float t, int r) {
         const int row = r + scatter_row<B>(lane);
-        // lane_val of lane (row - r0): a per-row value the caller loaded beforehand
-        const uint32_t v = (uint32_t)__shfl((int)lane_val, min(row - r0, 63));
-        if (lane < B && row < r1) epi(row, t, v);
+        const uint32_t v = KEEP ? (uint32_t)__shfl((int)*own, min(row - r0, 63)) : 0u;
+        uint32_t res = 0;
+        if (lane < B && row < r1) res = epi(row, t, v);
+        if constexpr (KEEP) {
+            const int k = r0 + lane - r;  // batch index of this lane's own row
+            const bool in = k >= 0 && k < B && r0 + lane < r1;
+            const uint32_t got = (uint32_t)__shfl((int)res, in ? scatter_row<B>(k) : 0);
+            if (in) *own = got;
+        }
+    };
+    if constexpr (STREAM) {
+        Rows<NC, B> nxt;
+        for (int r = r0; r < r1; r += 2 * B) {
+            if (r + B < r1) nxt.load(rowp, r + B, r1);
+            finish(batch_sums(cur, xin), r);
+            if (r + B >= r1) break;
+            if (r + 2 * B < r1) cur.load(rowp, r + 2 * B, r1);
+            finish(batch_sums(nxt, xin), r + B);
+        }
+    } else {
+        for (int r = r0; r < r1; r += B) {
+            if (r != r0) cur.load(rowp, r, r1);
+            finish(batch_sums(cur, xin), r);
+        }
     }
-}
-
-// Lane l < r1 - r0 (at most 64 rows): the bf16 bits of x[r0 + l], read coherently.
-__device__ __forceinline__ uint32_t load_rows_coh(const bf16 *x, int r0, int r1) {
-    const int lane = tid_x() & 63;
-    return r0 + lane < r1 ? ld_coh_bf16(x + r0 + lane) : 0u;
-}
-
-// The residual rows [r0, r1) of this wave before layer l's o rows. Layer 0 reads them from the
-// embedding row (the value workgroup 0 copies into x, which other workgroups may only read
-// after a completed barrier); later layers read x, whose rows this wave itself wrote last.
-__device__ __forceinline__ uint32_t residual_rows(KArgs &a, int l, int token, int H, int r0,
-                                                  int r1) {
-    if (l == 0) {
-        const int lane = tid_x() & 63;
-        const uint16_t *erow = (const uint16_t *)(a.embed + (size_t)token * H);
-        return r0 + lane < r1 ? (uint32_t)gptr(erow)[r0 + lane] : 0u;
-    }
-    return load_rows_coh(a.x, r0, r1);
 }
 
 // gate and up rows together (gate_up_kernel arithmetic); first batch preloaded.
@@ -259,38 +282,53 @@ __device__ __forceinline__ void wave_gemv2(const bf16 *Wg, const bf16 *Wu, int r
             gb.load([&](int rr) { return Wg + (size_t)rr * COLS; }, r, r1);
             ub.load([&](int rr) { return Wu + (size_t)rr * COLS; }, r, r1);
         }
-        float pg[B], pu[B];
-#pragma unroll
-        for (int i = 0; i < B; i++) {
-            float ag = 0.0f, au = 0.0f;
-#pragma unroll
-            for (int k = 0; k < NC; k++) {
-                ag = dot8(gb.w[i][k], xin[k], ag);
-                au = dot8(ub.w[i][k], xin[k], au);
-            }
-            pg[i] = ag;
-            pu[i] = au;
-        }
-        const float tg = wave_sum_scatter<B>(pg), tu = wave_sum_scatter<B>(pu);
+        const float tg = batch_sums(gb, xin), tu = batch_sums(ub, xin);
         const int row = r + scatter_row<B>(lane);
         if (lane < B && row < r1) epi(row, tg, tu);
     }
 }
 
+// Optional wall-clock stamps (trace != NULL). stamp: by thread 0 of the first matrix
+// workgroup, at index i. stamp_wg: for layer TRACE_LAYER only, by thread 0 of every
+// workgroup, at index 4 * n_layers + 3 + 8 * workgroup + k, with k = 2 * phase (input
+// staged) or 2 * phase + 1 (results stored); phase 0 is q/k/v (or a head's attention), then
+// o, gate/up, down.
+constexpr int TRACE_LAYER = 1;
+template <class S>
+__device__ __forceinline__ void stamp(int i) {
+    if (blockIdx.x == S::HQ && threadIdx.x == 0) {
+        long long *trace = kargs().trace;
+        if (trace) gptr(trace)[i] = wall_clock64();
+    }
+}
+__device__ __forceinline__ void stamp_wg(int l, int n_layers, int k) {
+    if (l == TRACE_LAYER) {
+        long long *trace = kargs().trace;
+        if (trace) {
+            if (k & 1) __syncthreads();  // "stored": when every wave has issued its stores
+            if (threadIdx.x == 0) gptr(trace)[4 * n_layers + 3 + 8 * blockIdx.x + k] = wall_clock64();
+        }
+    }
+}
+
+// ---------------------------------------------------------------- attention
 
 constexpr int PV_ROUND = 4;     // 64-position blocks per PV round (two per wave)
 constexpr int SCORE_LOADS = 8;  // keys per lane per scores round (8 * 4 * WAVES positions)
 
 // History keys (positions < pos, written by earlier steps) of the first scores round of one
-// head, loaded before the barrier that precedes attention. Slots at or beyond pos hold zeros;
-// attention_head substitutes the current position's key.
+// head, requested before its q/k/v are polled, and this lane's RoPE table entry at pos. Key
+// slots at or beyond pos hold zeros; attention_head substitutes the current position's key.
 struct AttnPrefetch {
     u32x4 k[SCORE_LOADS];
+    float cs[1], sn[1];
+    u32x4 wa, wb;  // wave 0: the q or k norm weight chunks of the lane's prologue slot
 };
 
 template <class S>
 struct AttnSmem {
     static constexpr int D = 128;
+    uint32_t raw[3][D / 2];         // the head's q, k and v rows as polled (bf16 pairs)
     u32x4 q[D / 8];                 // roped query head
     u32x4 k[D / 8];                 // roped key of the current position
     u32x4 v[D / 8];                 // value of the current position
@@ -301,10 +339,6 @@ struct AttnSmem {
     float out[D];                   // running sum over blocks
 };
 
-// One query head's attention at `pos` (attn_scores/pv/combine arithmetic, one workgroup):
-// wave 0 normalises and rotates q (and k, v for the workgroup that owns the cache write),
-// then scores, block statistics, the global max/sum, probabilities, PV per 64-position block
-// in four quarters, and the in-order combine.
 // Position of key slot u of this lane in the scores round starting at `base`, and of value
 // slot (j, it) in the PV round starting at block c0 (16 lanes per position, 8 waves).
 __device__ __forceinline__ int key_slot(int base, int u) {
@@ -316,22 +350,36 @@ __device__ __forceinline__ int value_slot(int c0, int j, int it) {
 }
 
 template <class S>
-__device__ __forceinline__ void attention_prefetch(KArgs &a, int h, int pos, int layer,
-                                                   AttnPrefetch &p) {
+__device__ __forceinline__ void attention_prefetch(KArgs &a, KLayer &L, int h, int pos,
+                                                   int layer, AttnPrefetch &p) {
     constexpr int D = 128, REP = S::HQ / S::HKV, KVD = S::HKV * D;
     const int g = h / REP, Lp = tid_x() & 15;
+    {
+        const int lane = tid_x() & 63, Lh = lane & 7;
+        const bf16 *nw = (lane >> 3) == 1 ? L.k_norm : L.q_norm;
+        p.wa = ld16(nw + 8 * Lh);
+        p.wb = ld16(nw + 64 + 8 * Lh);
+    }
     const bf16 *kc = a.key_cache + (size_t)layer * a.max_seq * KVD + g * D + 8 * Lp;
 #pragma unroll
     for (int u = 0; u < SCORE_LOADS; u++) {
         const int t = key_slot(0, u);
         p.k[u] = t < pos ? ld16_nt(kc + (size_t)t * KVD) : u32x4{0, 0, 0, 0};
     }
+    rope_table<D>(pos, a.inv_freq, p.cs, p.sn);
 }
 
+// One query head's attention at `pos` (attn_scores/pv/combine arithmetic, one workgroup): the
+// head's q and its group's k and v rows are polled (tag `tag_in`) into LDS; wave 0 normalises
+// and rotates q and k (the workgroup that owns the group writes k' and v into the cache);
+// then scores, block statistics, the global max/sum, probabilities, PV per 64-position block in
+// four quarters, and the in-order combine; the head's output is published with `tag_out`.
 template <class S>
 __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int pos, int layer,
-                               AttnSmem<S> &sm, AttnPrefetch &pre, bool prefetched) {
-    constexpr int D = 128, REP = S::HQ / S::HKV, KVD = S::HKV * D;
+                                               AttnSmem<S> &sm, AttnPrefetch &pre,
+                                               uint32_t tag_in, uint32_t tag_out,
+                                               int n_layers) {
+    constexpr int D = 128, REP = S::HQ / S::HKV, QD = S::HQ * D, KVD = S::HKV * D;
     const int lane = tid_x() & 63, w = tid_x() >> 6;
     const int g = h / REP;
     const bool owner = (h % REP) == 0;  // writes k', v into the cache
@@ -339,9 +387,21 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
     bf16 *vc = a.value_cache + (size_t)layer * a.max_seq * KVD;
     const int n = pos + 1;
     const int nb = (n + 63) / 64;
-    if (!prefetched) attention_prefetch<S>(a, h, pos, layer, pre);
     const u32x4 zero{0, 0, 0, 0};
-    // history values of the first PV round, requested now so their latency overlaps the
+
+    {
+        const uint32_t *qkv = a.tqkv;
+        const int qo = h * D, ko = QD + g * D, vo = QD + KVD + g * D;
+        stage_pairs<3 * D / 2>(
+            [=](int p) {
+                const int seg = p / (D / 2), i = 2 * (p % (D / 2));
+                return qkv + (seg == 0 ? qo : seg == 1 ? ko : vo) + i;
+            },
+            tag_in, &sm.raw[0][0], a.error_flag);
+    }
+    stamp_wg(layer, n_layers, 0);
+
+    // history values of a PV round; the first round is requested now and lands during the
     // prologue, the scores and the softmax
     u32x4 vv[PV_ROUND / 2][4];
     auto load_v = [&](int c0) {
@@ -359,12 +419,11 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
     if (w == 0) {
         // lanes 0-7: the query head, 8-15: the key head, 16-23: the value (copy only)
         const int slot = lane >> 3, Lh = lane & 7;
-        float cs[1], sn[1];
-        rope_table<D>(pos, a.inv_freq, cs, sn);
-        const bf16 *src = slot == 1 ? a.k + g * D : slot == 2 ? a.v + g * D : a.q + h * D;
-        const bf16 *nw = slot == 1 ? L.k_norm : L.q_norm;
-        const u32x4 xa = ld_coh16(src + 8 * Lh), xb = ld_coh16(src + 64 + 8 * Lh);
-        const u32x4 wa = ld16(nw + 8 * Lh), wb = ld16(nw + 64 + 8 * Lh);
+        const float (&cs)[1] = pre.cs, (&sn)[1] = pre.sn;
+        const int s3 = slot < 3 ? slot : 0;
+        const u32x4 xa = ((const u32x4 *)sm.raw[s3])[Lh];
+        const u32x4 xb = ((const u32x4 *)sm.raw[s3])[8 + Lh];
+        const u32x4 wa = pre.wa, wb = pre.wb;
         u32x4 ya, yb, oa, ob;
         norm_rope<D>(xa, xb, wa, wb, a.eps, cs, sn, Lh, ya, yb, oa, ob);
         const size_t row = (size_t)pos * KVD + g * D;
@@ -488,61 +547,73 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
         }
         __syncthreads();
     }
-    if (threadIdx.x < D) st_coh_bf16(a.attn_out + h * D + threadIdx.x, f2bf(sm.out[threadIdx.x]));
+    if (threadIdx.x < D)
+        put_tagged_all<QD>(a.tattn, h * D + threadIdx.x, f2bf(sm.out[threadIdx.x]), tag_out);
 }
 
 // ---------------------------------------------------------------- the step
 
-// Rows [r0, r1) of a phase with R rows owned by this wave. Wave 0 of each workgroup polls the
-// grid barrier and owns no rows: vector loads return in order, so a poller with weight loads
-// in flight would see the barrier only once they had landed.
-__device__ __forceinline__ void phase_rows(int R, int &r0, int &r1) {
-    const int w = __builtin_amdgcn_readfirstlane(tid_x() >> 6);
-    const int nw = gridDim.x * (WAVES - 1);
+// Rows [r0, r1) of a phase with R rows owned by wave w of this workgroup, the rows spread over
+// the waves of workgroups first_wg.. in order (so a workgroup owns rows iff its wave 0 does).
+__device__ __forceinline__ void phase_rows(int R, int first_wg, int w, int &r0, int &r1) {
+    const int nw = ((int)gridDim.x - first_wg) * WAVES;
     const int per = (R + nw - 1) / nw;
-    const int gw = blockIdx.x * (WAVES - 1) + w - 1;
-    r0 = w == 0 ? R : min(R, gw * per);
-    r1 = w == 0 ? R : min(R, r0 + per);
+    const int gw = ((int)blockIdx.x - first_wg) * WAVES + w;
+    const bool none = (int)blockIdx.x < first_wg;
+    r0 = none ? R : min(R, gw * per);
+    r1 = none ? R : min(R, r0 + per);
+}
+__device__ __forceinline__ void phase_rows(int R, int first_wg, int &r0, int &r1) {
+    phase_rows(R, first_wg, __builtin_amdgcn_readfirstlane(tid_x() >> 6), r0, r1);
+}
+__device__ __forceinline__ bool workgroup_has_rows(int R, int first_wg) {
+    int r0, r1;
+    phase_rows(R, first_wg, 0, r0, r1);
+    return r0 < r1;
 }
 
 template <class S>
 __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
     constexpr int H = S::H, I = S::I, D = 128, QD = S::HQ * D, KVD = S::HKV * D;
     constexpr int NCH = H / 512, NCO = QD / 512, NCI = I / 512;
-    __shared__ AttnSmem<S> sm;
+    constexpr int VEC_WORDS = (I > QD ? (I > H ? I : H) : (QD > H ? QD : H)) / 2;
+    __shared__ union Smem {
+        AttnSmem<S> attn;
+        uint32_t vec[VEC_WORDS];  // the staged input vector of a matrix phase (bf16 pairs)
+    } sm;
     __shared__ float red_v[WAVES];
     __shared__ int red_i[WAVES];
     __shared__ int last_wg;
-    const int lane = tid_x() & 63, w = tid_x() >> 6;
 
-    Barrier bar;
     int token, pos, n_layers;
+    unsigned seq0;  // tagged phases before this launch
     {
         KArgs &a = kargs();
-        bar.init(*gptr(a.epoch));
+        seq0 = *gptr(a.epoch);
         token = *gptr(a.next_token);
         pos = *gptr(a.pos);
         n_layers = a.n_layers;
         if (pos < 0 || pos >= a.max_seq || token < 0 || token >= a.vocab) {
             if (blockIdx.x == 0 && threadIdx.x == 0) *gptr(a.error_flag) = 1;
-            return;  // every workgroup reads the same values and leaves before any barrier
-        }
-        if (blockIdx.x == 0) {  // the residual stream starts as the embedding row
-            const bf16 *erow = a.embed + (size_t)token * H;
-            for (int c = threadIdx.x; c < H / 8; c += THREADS) {
-                const u32x4 v = ld16(erow + 8 * c);
-                st_coh64(a.x + 8 * c, (uint64_t)v.x | ((uint64_t)v.y << 32));
-                st_coh64(a.x + 8 * c + 4, (uint64_t)v.z | ((uint64_t)v.w << 32));
-            }
+            return;  // every workgroup reads the same values and leaves at once
         }
     }
+    stamp<S>(0);
 
-    // rows of each phase owned by this wave; o and down share the partition, so the residual
-    // rows a wave updates are its own (at most 64 per wave, checked by the host)
+    // Workgroups 0..HQ-1 run one query head's attention each and own no matrix rows; the
+    // others own the matrix rows and, while attention runs, load the weights of the o,
+    // gate/up and down rows. The o and down phases share the row partition, so the residual
+    // rows a wave updates are its own (at most 64 per wave, checked by the host). A
+    // workgroup reads a vector only when it owns rows that use it: then it produces part of
+    // what every later writer of that vector waits for, so it never sees a value overwritten.
+    const bool attn_wg = (int)blockIdx.x < S::HQ;
     int q0, q1, o0, o1, g0, g1;
-    phase_rows(QD + 2 * KVD, q0, q1);
-    phase_rows(H, o0, o1);
-    phase_rows(I, g0, g1);
+    phase_rows(QD + 2 * KVD, S::HQ, q0, q1);
+    phase_rows(H, S::HQ, o0, o1);
+    phase_rows(I, S::HQ, g0, g1);
+    const bool wg_q = workgroup_has_rows(QD + 2 * KVD, S::HQ);
+    const bool wg_o = workgroup_has_rows(H, S::HQ);
+    const bool wg_g = workgroup_has_rows(I, S::HQ);
 
     auto qkv_row = [](KLayer &L) {
         const bf16 *wq = L.wq, *wk = L.wk, *wv = L.wv;
@@ -551,145 +622,195 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                           : r < QD + KVD ? wk + (size_t)(r - QD) * H : wv + (size_t)(r - QD - KVD) * H;
         };
     };
-    auto residual = [](bf16 *x) {
+    auto o_row = [](KLayer &L) {
+        const bf16 *wo = L.wo;
+        return [=](int r) { return wo + (size_t)r * QD; };
+    };
+    auto d_row = [](KLayer &L) {
+        const bf16 *wd = L.w_down;
+        return [=](int r) { return wd + (size_t)r * I; };
+    };
+    auto residual = [](uint32_t *x, uint32_t tag) {
         return [=](int r, float y, uint32_t xr) {
-            st_coh_bf16(x + r, f2bf(bf2f((bf16)xr) + bf2f((bf16)f2bf(y))));
+            const uint32_t nb = f2bf(bf2f((bf16)xr) + bf2f((bf16)f2bf(y)));
+            put_tagged_all<H>(x, r, nb, tag);
+            return nb;
         };
     };
 
-    Rows<NCH, S::B_QKV> pf_qkv;
-    if (q0 < q1) pf_qkv.load(qkv_row(klayer(kargs(), 0)), q0, q1);
-
-    for (int l = 0;; l++) {
-        // ---- rmsnorm + q/k/v rows (weights prefetched during the previous barrier)
-        if (q0 < q1) {
-            KArgs &a = kargs();
-            KLayer &L = klayer(a, l);
-            u32x4 x[NCH], xb[NCH];
-            if (l == 0) {
-                const bf16 *erow = a.embed + (size_t)token * H;
-#pragma unroll
-                for (int k = 0; k < NCH; k++) x[k] = ld16(erow + 8 * (lane + 64 * k));
-            } else {
-                load_vec_coh<NCH>(a.x, x);
-            }
-            wave_rmsnorm<NCH>(x, L.attn_norm, a.eps, xb);
-            bf16 *q = a.q, *k = a.k, *v = a.v;
-            wave_gemv<NCH, S::B_QKV>(qkv_row(L), q0, q1, xb, pf_qkv, [=](int r, float y, uint32_t) {
-                bf16 *dst = r < QD ? q + r : r < QD + KVD ? k + (r - QD) : v + (r - QD - KVD);
-                st_coh_bf16(dst, f2bf(y));
-            });
-        }
-        // ---- QK-norm + RoPE + KV write + attention, one workgroup per query head. Attention
-        // workgroups load their first K/V history rounds during the barrier and the o weights
-        // after attention; the others load the o weights at once. Both paths pass two barriers.
-        Rows<NCO, S::B_O> pf_o;
-        auto o_row = [](KLayer &L) {
-            const bf16 *wo = L.wo;
-            return [=](int r) { return wo + (size_t)r * QD; };
-        };
-        uint32_t xres;
-        if (blockIdx.x < S::HQ) {
-            AttnPrefetch pre;
-            bar.arrive();
-            attention_prefetch<S>(kargs(), blockIdx.x, opaque(pos), l, pre);
-            bar.wait();
+    // tags of layer l: seq q|k|v, seq+1 attention, seq+2 x after o, seq+3 SwiGLU, seq+4 x
+    // after down, with seq = seq0 + PHASES * l
+    if (attn_wg) {
+        // ---- QK-norm + RoPE + KV write + attention, one query head per workgroup
+        for (int l = 0; l < n_layers; l++) {
+            const unsigned seq = seq0 + PHASES * l;
             for (int h = blockIdx.x; h < S::HQ; h += gridDim.x) {
                 KArgs &a = kargs();
-                attention_head<S>(a, klayer(a, l), h, opaque(pos), l, sm, pre,
-                                  h == (int)blockIdx.x);
+                AttnPrefetch pre;
+                attention_prefetch<S>(a, klayer(a, l), h, opaque(pos), l, pre);
+                attention_head<S>(a, klayer(a, l), h, opaque(pos), l, sm.attn, pre,
+                                  tag_of(seq), tag_of(seq + 1), n_layers);
+                stamp_wg(l, n_layers, 1);
             }
-            bar.arrive();
-            if (o0 < o1) pf_o.load(o_row(klayer(kargs(), l)), o0, o1);
-            xres = residual_rows(kargs(), l, token, H, o0, o1);
-            bar.wait();
-        } else {
-            bar.arrive();
-            if (o0 < o1) pf_o.load(o_row(klayer(kargs(), l)), o0, o1);
-            xres = residual_rows(kargs(), l, token, H, o0, o1);
-            bar.wait();
-            bar.arrive();
-            bar.wait();
         }
-        // ---- o rows + residual
+    } else {
+        // the wave's residual rows of x (lane j: row o0 + j), starting as the embedding row
+        uint32_t xown = 0;
         if (o0 < o1) {
-            u32x4 in[NCO];
-            load_vec_coh<NCO>(kargs().attn_out, in);
-            wave_gemv<NCO, S::B_O>(o_row(klayer(kargs(), l)), o0, o1, in, pf_o,
-                                   residual(kargs().x), xres);
+            const int lane = tid_x() & 63;
+            const uint16_t *erow = (const uint16_t *)(kargs().embed + (size_t)token * H);
+            xown = o0 + lane < o1 ? (uint32_t)gptr(erow)[o0 + lane] : 0u;
         }
-        Rows<NCH, S::B_GU> pf_g, pf_u;
-        bar.arrive();
-        if (g0 < g1) {
-            KLayer &L = klayer(kargs(), l);
-            const bf16 *wg = L.w_gate, *wu = L.w_up;
-            pf_g.load([=](int r) { return wg + (size_t)r * H; }, g0, g1);
-            pf_u.load([=](int r) { return wu + (size_t)r * H; }, g0, g1);
+        Rows<NCH, S::B_QKV> pf_qkv;
+        u32x4 nq[NCH];  // attn_norm chunks of the coming q/k/v phase
+        if (q0 < q1) {
+            pf_qkv.load(qkv_row(klayer(kargs(), 0)), q0, q1);
+            load_chunks<NCH>(klayer(kargs(), 0).attn_norm, nq);
         }
-        bar.wait();
-        // ---- rmsnorm + gate/up rows + SwiGLU
-        if (g0 < g1) {
-            KArgs &a = kargs();
-            KLayer &L = klayer(a, l);
-            u32x4 x[NCH], xb[NCH];
-            load_vec_coh<NCH>(a.x, x);
-            wave_rmsnorm<NCH>(x, L.mlp_norm, a.eps, xb);
-            bf16 *hb = a.hb;
-            wave_gemv2<NCH, S::B_GU>(L.w_gate, L.w_up, g0, g1, xb, pf_g, pf_u,
-                                     [=](int r, float g, float u) {
-                const bf16 gb = (bf16)f2bf(g), ub = (bf16)f2bf(u);
-                const float s = round_bf(silu_f32(bf2f(gb)));
-                st_coh_bf16(hb + r, f2bf(s * bf2f(ub)));
-            });
+        for (int l = 0; l < n_layers; l++) {
+            const unsigned seq = seq0 + PHASES * l;
+            // ---- rmsnorm + q/k/v rows (weights requested a phase ahead)
+            if (wg_q) {
+                if (l == 0) {
+                    stage_plain<H>(kargs().embed + (size_t)token * H, sm.vec);
+                } else {
+                    stage_vector<H>(my_copy<H>(kargs().tx), tag_of(seq - 1), sm.vec,
+                                    kargs().error_flag);
+                }
+            }
+            stamp<S>(1 + 4 * l);
+            stamp_wg(l, n_layers, 0);
+            if (q0 < q1) {
+                KArgs &a = kargs();
+                KLayer &L = klayer(a, l);
+                u32x4 x[NCH], xb[NCH];
+                lds_chunks<NCH>(sm.vec, x);
+                wave_rmsnorm<NCH>(x, nq, a.eps, xb);
+                uint32_t *out = a.tqkv;
+                const uint32_t tag = tag_of(seq);
+                wave_gemv<NCH, S::B_QKV, false>(qkv_row(L), q0, q1, xb, pf_qkv,
+                                                [=](int r, float y, uint32_t) {
+                                                    const uint32_t b = f2bf(y);
+                                                    put_tagged(out, r, b, tag);
+                                                    return b;
+                                                });
+            }
+            stamp_wg(l, n_layers, 1);
+            // weights of the next phases, loaded while attention runs
+            Rows<NCO, S::B_O> pf_o;
+            Rows<NCH, S::B_GU> pf_g, pf_u;
+            Rows<NCI, S::B_DOWN> pf_d;
+            u32x4 ng[NCH];  // mlp_norm chunks
+            if (o0 < o1) pf_o.load(o_row(klayer(kargs(), l)), o0, o1);
+            if (g0 < g1) {
+                KLayer &L = klayer(kargs(), l);
+                const bf16 *wg = L.w_gate, *wu = L.w_up;
+                pf_g.load([=](int r) { return wg + (size_t)r * H; }, g0, g1);
+                pf_u.load([=](int r) { return wu + (size_t)r * H; }, g0, g1);
+                load_chunks<NCH>(L.mlp_norm, ng);
+            }
+            if constexpr (S::PF_EARLY) {
+                if (o0 < o1) pf_d.load(d_row(klayer(kargs(), l)), o0, o1);
+                if (q0 < q1 && l + 1 < n_layers) {
+                    pf_qkv.load(qkv_row(klayer(kargs(), l + 1)), q0, q1);
+                    load_chunks<NCH>(klayer(kargs(), l + 1).attn_norm, nq);
+                }
+            }
+            // ---- o rows + residual
+            if (wg_o)
+                stage_vector<QD>(my_copy<QD>(kargs().tattn), tag_of(seq + 1), sm.vec,
+                                 kargs().error_flag);
+            stamp<S>(2 + 4 * l);
+            stamp_wg(l, n_layers, 2);
+            if (o0 < o1) {
+                u32x4 in[NCO];
+                lds_chunks<NCO>(sm.vec, in);
+                wave_gemv<NCO, S::B_O, S::O_STREAM, true>(o_row(klayer(kargs(), l)), o0, o1, in,
+                                                          pf_o, residual(kargs().tx, tag_of(seq + 2)),
+                                                          &xown);
+            }
+            stamp_wg(l, n_layers, 3);
+            // ---- rmsnorm + gate/up rows + SwiGLU
+            if (wg_g)
+                stage_vector<H>(my_copy<H>(kargs().tx), tag_of(seq + 2), sm.vec, kargs().error_flag);
+            stamp<S>(3 + 4 * l);
+            stamp_wg(l, n_layers, 4);
+            if (g0 < g1) {
+                KArgs &a = kargs();
+                KLayer &L = klayer(a, l);
+                u32x4 x[NCH], xb[NCH];
+                lds_chunks<NCH>(sm.vec, x);
+                wave_rmsnorm<NCH>(x, ng, a.eps, xb);
+                uint32_t *hb = a.thb;
+                const uint32_t tag = tag_of(seq + 3);
+                wave_gemv2<NCH, S::B_GU>(L.w_gate, L.w_up, g0, g1, xb, pf_g, pf_u,
+                                         [=](int r, float g, float u) {
+                    const bf16 gb = (bf16)f2bf(g), ub = (bf16)f2bf(u);
+                    const float s = round_bf(silu_f32(bf2f(gb)));
+                    put_tagged_all<I>(hb, r, f2bf(s * bf2f(ub)), tag);
+                });
+            }
+            stamp_wg(l, n_layers, 5);
+            if constexpr (!S::PF_EARLY) {
+                if (o0 < o1) pf_d.load(d_row(klayer(kargs(), l)), o0, o1);
+            }
+            // ---- down rows + residual
+            if (wg_o)
+                stage_vector<I>(my_copy<I>(kargs().thb), tag_of(seq + 3), sm.vec, kargs().error_flag);
+            stamp<S>(4 + 4 * l);
+            stamp_wg(l, n_layers, 6);
+            if (o0 < o1) {
+                u32x4 in[NCI];
+                lds_chunks<NCI>(sm.vec, in);
+                wave_gemv<NCI, S::B_DOWN, S::D_STREAM, true>(d_row(klayer(kargs(), l)), o0, o1,
+                                                             in, pf_d,
+                                                             residual(kargs().tx, tag_of(seq + 4)),
+                                                             &xown);
+            }
+            stamp_wg(l, n_layers, 7);
+            if constexpr (!S::PF_EARLY) {
+                if (q0 < q1 && l + 1 < n_layers) {
+                    pf_qkv.load(qkv_row(klayer(kargs(), l + 1)), q0, q1);
+                    load_chunks<NCH>(klayer(kargs(), l + 1).attn_norm, nq);
+                }
+            }
         }
-        Rows<NCI, S::B_DOWN> pf_d;
-        auto d_row = [](KLayer &L) {
-            const bf16 *wd = L.w_down;
-            return [=](int r) { return wd + (size_t)r * I; };
-        };
-        bar.arrive();
-        if (o0 < o1) pf_d.load(d_row(klayer(kargs(), l)), o0, o1);
-        xres = load_rows_coh(kargs().x, o0, o1);
-        bar.wait();
-        // ---- down rows + residual
-        if (o0 < o1) {
-            u32x4 in[NCI];
-            load_vec_coh<NCI>(kargs().hb, in);
-            wave_gemv<NCI, S::B_DOWN>(d_row(klayer(kargs(), l)), o0, o1, in, pf_d,
-                                      residual(kargs().x), xres);
-        }
-        if (l + 1 == n_layers) break;
-        bar.arrive();
-        if (q0 < q1) pf_qkv.load(qkv_row(klayer(kargs(), l + 1)), q0, q1);
-        bar.wait();
     }
 
-    // ---- final rmsnorm + LM head + argmax (the first batch of LM-head rows is loaded during
-    // the last barrier)
+    // ---- final rmsnorm + LM head + argmax over every workgroup (two batches of LM-head rows
+    // in flight; the first is requested before the residual stream is polled)
     {
+        const unsigned seq_end = seq0 + PHASES * n_layers;
         int r0, r1;
-        phase_rows(kargs().vocab, r0, r1);
+        phase_rows(kargs().vocab, 0, r0, r1);
         const bf16 *lm = kargs().lm_head;
         auto lm_row = [=](int r) { return lm + (size_t)r * H; };
         Rows<NCH, S::B_LM> batch;
-        bar.arrive();
-        if (r0 < r1) batch.load(lm_row, r0, r1);
-        bar.wait();
+        u32x4 nf[NCH];  // final_norm chunks
+        if (r0 < r1) {
+            batch.load(lm_row, r0, r1);
+            load_chunks<NCH>(kargs().final_norm, nf);
+        }
+        stage_vector<H>(my_copy<H>(kargs().tx), tag_of(seq_end - 1), sm.vec, kargs().error_flag);
+        stamp<S>(1 + 4 * n_layers);
         float best = -__builtin_huge_valf();
         int bidx = INT_MAX;
         if (r0 < r1) {
             KArgs &a = kargs();
             u32x4 x[NCH], xb[NCH];
-            load_vec_coh<NCH>(a.x, x);
-            wave_rmsnorm<NCH>(x, a.final_norm, a.eps, xb);
+            lds_chunks<NCH>(sm.vec, x);
+            wave_rmsnorm<NCH>(x, nf, a.eps, xb);
             bf16 *logits = a.logits;
-            wave_gemv<NCH, S::B_LM>(lm_row, r0, r1, xb, batch, [&](int r, float y, uint32_t) {
+            wave_gemv<NCH, S::B_LM, true>(lm_row, r0, r1, xb, batch,
+                                          [&](int r, float y, uint32_t) {
                 const uint32_t yb = f2bf(y);
                 gptr(logits)[r] = (bf16)yb;
                 amax_pair(best, bidx, bf2f((bf16)yb), r);
+                return yb;
             });
         }
         wave_amax(best, bidx);
+        const int lane = tid_x() & 63, w = tid_x() >> 6;
         if (lane == 0) {
             red_v[w] = best;
             red_i[w] = bidx;
@@ -729,8 +850,8 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                     *gptr(a.pos) = pos + 1;
                 }
                 *gptr(a.final_ctr) = 0;
-                *gptr(a.epoch) = bar.epoch;
-                if (a.trace) gptr(a.trace)[bar.n + 1] = wall_clock64();
+                *gptr(a.epoch) = seq_end;
+                if (a.trace) gptr(a.trace)[2 + 4 * n_layers] = wall_clock64();
             }
         }
     }
@@ -742,16 +863,21 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
 // host side
 // ------------------------------------------------------------------------------------------
 
-// Compile-time shapes with the per-phase rows-per-batch choices (VGPR budget of 2 waves/SIMD).
+// Compile-time shapes with the per-phase rows-per-batch choices (VGPR budget of 2 waves/SIMD)
+// for a grid of 256 workgroups: the matrix rows spread over (256 - HQ) * 8 waves. PF_EARLY:
+// the down rows and the next layer's q/k/v rows are also requested while attention runs.
 template <int H_, int I_, int HQ_, int HKV_>
 struct Shape {
     static constexpr int H = H_, I = I_, HQ = HQ_, HKV = HKV_;
     static constexpr int NMAX = 8192;  // positions a query head attends over (LDS scores)
     static constexpr int B_QKV = H <= 1024 ? 4 : 2;
-    static constexpr int B_O = HQ * 128 <= 2048 ? 2 : 1;
+    static constexpr int B_O = H <= 1024 ? 1 : (HQ * 128 <= 2048 ? 2 : 1);
     static constexpr int B_GU = H <= 1024 ? 2 : 1;
     static constexpr int B_DOWN = 1;
     static constexpr int B_LM = H <= 1024 ? 8 : (H <= 2048 ? 4 : 2);
+    static constexpr bool PF_EARLY = H <= 1024;
+    static constexpr bool O_STREAM = H > 1024;
+    static constexpr bool D_STREAM = H > 1024;
 };
 
 using Qwen3_06B = Shape<1024, 3072, 16, 8>;
@@ -770,8 +896,26 @@ static const void *step_kernel_for(const Config *c) {
     return nullptr;
 }
 
+// The kernel's layout needs workgroups beyond the attention ones (at least as many again) and
+// at most 64 residual rows per matrix wave.
+static bool step_grid_fits(const Config *c, int grid) {
+    if (grid <= 0 || grid > 1024 || grid < 2 * c->n_heads) return false;
+    const int waves = (grid - c->n_heads) * WAVES;
+    return (c->hidden_size + waves - 1) / waves <= 64;
+}
+
+size_t step_workspace_bytes(const Config *c) {
+    const size_t qd = (size_t)c->n_heads * c->head_dim, kvd = (size_t)c->n_kv_heads * c->head_dim;
+    const size_t words = STEP_REPLICAS * step_replica_stride(c->hidden_size) +
+                         step_replica_stride(qd + 2 * kvd) +
+                         STEP_REPLICAS * step_replica_stride(qd) +
+                         STEP_REPLICAS * step_replica_stride(c->intermediate_size);
+    return sizeof(StepWorkspace) + 4 * words;
+}
+
 bool step_kernel_supported(const Config *cfg, int max_seq) {
-    return step_kernel_for(cfg) != nullptr && max_seq <= 8192 && cfg->vocab_size > 0;
+    return step_kernel_for(cfg) != nullptr && max_seq <= 8192 && cfg->vocab_size > 0 &&
+           step_grid_fits(cfg, step_kernel_grid());
 }
 
 int step_kernel_grid() {
@@ -779,12 +923,13 @@ int step_kernel_grid() {
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
         return 0;
-    return cus;
+    return cus > 1024 ? 1024 : cus;
 }
 
 bool step_kernel_launch(const Config *cfg, const StepArgs &args, int grid, hipStream_t stream) {
     const void *fn = step_kernel_for(cfg);
     if (!fn) return llm_fail("step kernel: no specialisation for these shapes");
+    if (!step_grid_fits(cfg, grid)) return llm_fail("step kernel: grid of %d does not fit", grid);
     StepArgs a = args;
     void *params[] = {&a};
     return HIP_OK(hipLaunchCooperativeKernel(fn, dim3(grid), dim3(THREADS), params, 0, stream));
