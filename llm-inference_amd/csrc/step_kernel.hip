@@ -321,8 +321,8 @@ constexpr int SCORE_LOADS = 8;  // keys per lane per scores round (8 * 4 * WAVES
 // slots at or beyond pos hold zeros; attention_head substitutes the current position's key.
 struct AttnPrefetch {
     u32x4 k[SCORE_LOADS];
-    float cs[1], sn[1];
-    u32x4 wa, wb;  // wave 0: the q or k norm weight chunks of the lane's prologue slot
+    float cs[1], sn[1];  // RoPE table entry `lane` (rotation pair lane, lane + 64)
+    float w0, w1;        // waves 0/1: q/k norm weights of elements lane and lane + 64
 };
 
 template <class S>
@@ -355,10 +355,10 @@ __device__ __forceinline__ void attention_prefetch(KArgs &a, KLayer &L, int h, i
     constexpr int D = 128, REP = S::HQ / S::HKV, KVD = S::HKV * D;
     const int g = h / REP, Lp = tid_x() & 15;
     {
-        const int lane = tid_x() & 63, Lh = lane & 7;
-        const bf16 *nw = (lane >> 3) == 1 ? L.k_norm : L.q_norm;
-        p.wa = ld16(nw + 8 * Lh);
-        p.wb = ld16(nw + 64 + 8 * Lh);
+        const int lane = tid_x() & 63;
+        const uint16_t *nw = (const uint16_t *)((tid_x() >> 6) == 1 ? L.k_norm : L.q_norm);
+        p.w0 = bf2f(gptr(nw)[lane]);
+        p.w1 = bf2f(gptr(nw)[64 + lane]);
     }
     const bf16 *kc = a.key_cache + (size_t)layer * a.max_seq * KVD + g * D + 8 * Lp;
 #pragma unroll
@@ -367,6 +367,8 @@ __device__ __forceinline__ void attention_prefetch(KArgs &a, KLayer &L, int h, i
         p.k[u] = t < pos ? ld16_nt(kc + (size_t)t * KVD) : u32x4{0, 0, 0, 0};
     }
     rope_table<D>(pos, a.inv_freq, p.cs, p.sn);
+    // computed here, before the workgroup waits for its q/k/v, not sunk to the first use
+    asm volatile("" : "+v"(p.cs[0]), "+v"(p.sn[0]));
 }
 
 // One query head's attention at `pos` (attn_scores/pv/combine arithmetic, one workgroup): the
@@ -416,33 +418,52 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
     };
     load_v(0);
 
-    if (w == 0) {
-        // lanes 0-7: the query head, 8-15: the key head, 16-23: the value (copy only)
-        const int slot = lane >> 3, Lh = lane & 7;
-        const float (&cs)[1] = pre.cs, (&sn)[1] = pre.sn;
-        const int s3 = slot < 3 ? slot : 0;
-        const u32x4 xa = ((const u32x4 *)sm.raw[s3])[Lh];
-        const u32x4 xb = ((const u32x4 *)sm.raw[s3])[8 + Lh];
-        const u32x4 wa = pre.wa, wb = pre.wb;
-        u32x4 ya, yb, oa, ob;
-        norm_rope<D>(xa, xb, wa, wb, a.eps, cs, sn, Lh, ya, yb, oa, ob);
+    // QK-norm + RoPE (qk_norm_rope_kernel arithmetic): wave 0 the query head, wave 1 the key
+    // head, wave 2 copies the value row. Lane i holds elements i and i + 64, the pair RoPE
+    // rotates with table entry i; lanes 0-7 form the sum of squares in the order of the
+    // standalone kernel (elements 8L.. then 64+8L.., then the 8-lane tree).
+    if (w < 3) {
+        const uint16_t *x16 = (const uint16_t *)sm.raw[w];
+        const uint32_t xi = x16[lane], xj = x16[64 + lane];
         const size_t row = (size_t)pos * KVD + g * D;
-        if (slot == 0) {
-            sm.q[Lh] = oa;
-            sm.q[8 + Lh] = ob;
-        } else if (slot == 1) {
-            sm.k[Lh] = oa;
-            sm.k[8 + Lh] = ob;
-            if (owner) {
-                st16(kc + row + 8 * Lh, oa);
-                st16(kc + row + 64 + 8 * Lh, ob);
+        if (w < 2) {
+            float acc = 0.0f;
+            {
+                const int L8 = (lane & 7) * 8;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float v = bf2f((bf16)x16[L8 + e]);
+                    acc = fmaf(v, v, acc);
+                }
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float v = bf2f((bf16)x16[64 + L8 + e]);
+                    acc = fmaf(v, v, acc);
+                }
             }
-        } else if (slot == 2) {
-            sm.v[Lh] = xa;
-            sm.v[8 + Lh] = xb;
+            const float total = __uint_as_float(
+                __builtin_amdgcn_readfirstlane(__float_as_uint(group_sum<8>(acc))));
+            const float inv = 1.0f / sqrtf(total / (float)D + a.eps);
+            const float ya = round_bf(round_bf(bf2f((bf16)xi) * inv) * pre.w0);
+            const float yb = round_bf(round_bf(bf2f((bf16)xj) * inv) * pre.w1);
+            const float c = pre.cs[0], sn = pre.sn[0];
+            const float a_cos = round_bf(ya * c), b_sin = round_bf(yb * sn);
+            const float b_cos = round_bf(yb * c), a_sin = round_bf(ya * sn);
+            const uint32_t oa = f2bf(a_cos - b_sin), ob = f2bf(b_cos + a_sin);
+            uint16_t *dst = (uint16_t *)(w == 0 ? sm.q : sm.k);
+            dst[lane] = (uint16_t)oa;
+            dst[64 + lane] = (uint16_t)ob;
+            if (w == 1 && owner) {
+                gptr((uint16_t *)(kc + row))[lane] = (uint16_t)oa;
+                gptr((uint16_t *)(kc + row))[64 + lane] = (uint16_t)ob;
+            }
+        } else {
+            uint16_t *dst = (uint16_t *)sm.v;
+            dst[lane] = (uint16_t)xi;
+            dst[64 + lane] = (uint16_t)xj;
             if (owner) {
-                st16(vc + row + 8 * Lh, xa);
-                st16(vc + row + 64 + 8 * Lh, xb);
+                gptr((uint16_t *)(vc + row))[lane] = (uint16_t)xi;
+                gptr((uint16_t *)(vc + row))[64 + lane] = (uint16_t)xj;
             }
         }
     }
@@ -464,6 +485,7 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
             }
 #pragma unroll
             for (int u = 0; u < SCORE_LOADS; u++) {
+                if (base + u * 4 * WAVES >= n) break;  // the rest of the round is past pos
                 const int t = key_slot(base, u);
                 const float d = group_sum<16>(dot8(qv, kv[u], 0.0f));
                 const float s = round_bf(round_bf(d) * a.scale);
@@ -472,6 +494,19 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
         }
     }
     __syncthreads();
+    if (nb == 1) {
+        // one block: its max and sum are the global ones (its weight exp(0) is exactly 1), so
+        // wave 0 finishes the softmax alone
+        if (w == 0) {
+            const bool v = lane < n;
+            const float s = v ? sm.sc[lane] : -__builtin_huge_valf();
+            const float M = wave_max(s);
+            const float e = v ? exp_f32(s - M) : 0.0f;
+            const float sum = wave_sum(e);
+            if (v) sm.sc[lane] = round_bf(exp_f32(s - M) / sum);
+        }
+        __syncthreads();
+    } else {
     // block statistics
     for (int b = w; b < nb; b += WAVES) {
         const bool v = b * 64 + lane < n;
@@ -509,6 +544,7 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
         for (int t = threadIdx.x; t < n; t += THREADS) sm.sc[t] = round_bf(exp_f32(sm.sc[t] - M) / sum);
     }
     __syncthreads();
+    }
     // PV in rounds of PV_ROUND blocks: wave w takes blocks c0 + w/4 + 2j and quarter w % 4 of
     // each (slots quarter*16 + it*4 + G); the quarters meet in order, the blocks are added in order
     const u32x4 vcur = sm.v[Lp];
@@ -516,6 +552,7 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
         if (c0 > 0) load_v(c0);
 #pragma unroll
         for (int j = 0; j < PV_ROUND / 2; j++) {
+            if (c0 + (w >> 2) + 2 * j >= nb) break;  // block past pos
             float acc[8];
 #pragma unroll
             for (int e = 0; e < 8; e++) acc[e] = 0.0f;
