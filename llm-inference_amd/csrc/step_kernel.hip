@@ -169,33 +169,48 @@ __device__ __forceinline__ void lds_chunks(const uint32_t *vec, u32x4 (&out)[NC]
     for (int k = 0; k < NC; k++) out[k] = ((const u32x4 *)vec)[lane + 64 * k];
 }
 
-// This lane's chunks (lane + 64k) of a vector in global memory (norm weights: plain loads, so
-// they stay cached from one step to the next).
-template <int NC>
-__device__ __forceinline__ void load_chunks(const bf16 *v, u32x4 (&out)[NC]) {
-    const int lane = tid_x() & 63;
+// Norm weights of the elements this thread normalises in wg_rmsnorm: i = threadIdx.x +
+// THREADS * j.
+template <int N>
+struct NormW {
+    static constexpr int E = (N + THREADS - 1) / THREADS;
+    float w[E];
+    __device__ __forceinline__ void load(const bf16 *g) {
+        const uint16_t *g16 = (const uint16_t *)g;
 #pragma unroll
-    for (int k = 0; k < NC; k++) out[k] = ld16(v + 8 * (lane + 64 * k));
-}
-
-// RMSNorm of a row of 512*NC elements held as chunks, with the weight chunks wn
-// (rmsnorm_wave_kernel arithmetic).
-template <int NC>
-__device__ __forceinline__ void wave_rmsnorm(const u32x4 (&x)[NC], const u32x4 (&wn)[NC],
-                                             float eps, u32x4 (&out)[NC]) {
-    float acc = 0.0f;
-#pragma unroll
-    for (int k = 0; k < NC; k++) acc = dot8(x[k], x[k], acc);
-    const float total = wave_sum(acc);
-    const float inv = 1.0f / sqrtf(total / (float)(512 * NC) + eps);
-#pragma unroll
-    for (int k = 0; k < NC; k++) {
-        const u32x4 wv = wn[k];
-        float r[8];
-#pragma unroll
-        for (int e = 0; e < 8; e++) r[e] = round_bf(elem(x[k], e) * inv) * elem(wv, e);
-        out[k] = u32x4{pack2(r[0], r[1]), pack2(r[2], r[3]), pack2(r[4], r[5]), pack2(r[6], r[7])};
+        for (int j = 0; j < E; j++) {
+            const int i = threadIdx.x + THREADS * j;
+            w[j] = i < N ? bf2f(gptr(g16)[i]) : 0.0f;
+        }
     }
+};
+
+// RMSNorm of the staged vector (LDS, bf16), in place, once per workgroup with the arithmetic of
+// rmsnorm_wave_kernel: wave 0 forms the sum of squares (lane l: chunks l + 64k in order, then the
+// wave tree), every thread then normalises its elements as bf16(bf16(x * inv) * gamma). Ends with
+// a workgroup sync.
+template <int N>
+__device__ __forceinline__ void wg_rmsnorm(uint32_t *vec, const NormW<N> &nw, float eps,
+                                           float *inv_slot) {
+    constexpr int NC = N / 512;
+    if ((tid_x() >> 6) == 0) {
+        u32x4 x[NC];
+        lds_chunks<NC>(vec, x);
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < NC; k++) acc = dot8(x[k], x[k], acc);
+        const float total = wave_sum(acc);
+        if ((tid_x() & 63) == 0) *inv_slot = 1.0f / sqrtf(total / (float)N + eps);
+    }
+    __syncthreads();
+    const float inv = *inv_slot;
+    uint16_t *v16 = (uint16_t *)vec;
+#pragma unroll
+    for (int j = 0; j < NormW<N>::E; j++) {
+        const int i = threadIdx.x + THREADS * j;
+        if (i < N) v16[i] = (uint16_t)f2bf(round_bf(bf2f((bf16)v16[i]) * inv) * nw.w[j]);
+    }
+    __syncthreads();
 }
 
 // B rows of NC chunks each, held in registers: lane l has chunk l + 64k of every row. `rowp`
@@ -506,6 +521,29 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
             if (v) sm.sc[lane] = round_bf(exp_f32(s - M) / sum);
         }
         __syncthreads();
+    } else if (nb <= WAVES) {
+        // up to 8 blocks: wave b takes block b's statistics; after one sync every wave forms
+        // the global max and sum from the nb pairs (lane b: block b, the order of the general
+        // path below) and writes its block's probabilities
+        const bool v = w < nb && w * 64 + lane < n;
+        const float s = v ? sm.sc[w * 64 + lane] : -__builtin_huge_valf();
+        if (w < nb) {
+            const float m = wave_max(s);
+            const float e = v ? exp_f32(s - m) : 0.0f;
+            const float Ssum = wave_sum(e);
+            if (lane == 0) {
+                sm.st[w][0] = m;
+                sm.st[w][1] = Ssum;
+            }
+        }
+        __syncthreads();
+        if (w < nb) {
+            const float M = wave_max(lane < nb ? sm.st[lane][0] : -__builtin_huge_valf());
+            const float sum =
+                wave_sum(lane < nb ? sm.st[lane][1] * exp_f32(sm.st[lane][0] - M) : 0.0f);
+            if (v) sm.sc[w * 64 + lane] = round_bf(exp_f32(s - M) / sum);
+        }
+        __syncthreads();
     } else {
     // block statistics
     for (int b = w; b < nb; b += WAVES) {
@@ -621,6 +659,7 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
     __shared__ float red_v[WAVES];
     __shared__ int red_i[WAVES];
     __shared__ int last_wg;
+    __shared__ float norm_inv;
 
     int token, pos, n_layers;
     unsigned seq0;  // tagged phases before this launch
@@ -699,11 +738,9 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
             xown = o0 + lane < o1 ? (uint32_t)gptr(erow)[o0 + lane] : 0u;
         }
         Rows<NCH, S::B_QKV> pf_qkv;
-        u32x4 nq[NCH];  // attn_norm chunks of the coming q/k/v phase
-        if (q0 < q1) {
-            pf_qkv.load(qkv_row(klayer(kargs(), 0)), q0, q1);
-            load_chunks<NCH>(klayer(kargs(), 0).attn_norm, nq);
-        }
+        NormW<H> nq;  // attn_norm weights of the coming q/k/v phase
+        if (wg_q) nq.load(klayer(kargs(), 0).attn_norm);
+        if (q0 < q1) pf_qkv.load(qkv_row(klayer(kargs(), 0)), q0, q1);
         for (int l = 0; l < n_layers; l++) {
             const unsigned seq = seq0 + PHASES * l;
             // ---- rmsnorm + q/k/v rows (weights requested a phase ahead)
@@ -717,12 +754,12 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
             }
             stamp<S>(1 + 4 * l);
             stamp_wg(l, n_layers, 0);
+            if (wg_q) wg_rmsnorm<H>(sm.vec, nq, kargs().eps, &norm_inv);
             if (q0 < q1) {
                 KArgs &a = kargs();
                 KLayer &L = klayer(a, l);
-                u32x4 x[NCH], xb[NCH];
-                lds_chunks<NCH>(sm.vec, x);
-                wave_rmsnorm<NCH>(x, nq, a.eps, xb);
+                u32x4 xb[NCH];
+                lds_chunks<NCH>(sm.vec, xb);
                 uint32_t *out = a.tqkv;
                 const uint32_t tag = tag_of(seq);
                 wave_gemv<NCH, S::B_QKV, false>(qkv_row(L), q0, q1, xb, pf_qkv,
@@ -737,21 +774,20 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
             Rows<NCO, S::B_O> pf_o;
             Rows<NCH, S::B_GU> pf_g, pf_u;
             Rows<NCI, S::B_DOWN> pf_d;
-            u32x4 ng[NCH];  // mlp_norm chunks
+            NormW<H> ng;  // mlp_norm weights
             if (o0 < o1) pf_o.load(o_row(klayer(kargs(), l)), o0, o1);
+            if (wg_g) ng.load(klayer(kargs(), l).mlp_norm);
             if (g0 < g1) {
                 KLayer &L = klayer(kargs(), l);
                 const bf16 *wg = L.w_gate, *wu = L.w_up;
                 pf_g.load([=](int r) { return wg + (size_t)r * H; }, g0, g1);
                 pf_u.load([=](int r) { return wu + (size_t)r * H; }, g0, g1);
-                load_chunks<NCH>(L.mlp_norm, ng);
             }
             if constexpr (S::PF_EARLY) {
                 if (o0 < o1) pf_d.load(d_row(klayer(kargs(), l)), o0, o1);
-                if (q0 < q1 && l + 1 < n_layers) {
+                if (wg_q && l + 1 < n_layers) nq.load(klayer(kargs(), l + 1).attn_norm);
+                if (q0 < q1 && l + 1 < n_layers)
                     pf_qkv.load(qkv_row(klayer(kargs(), l + 1)), q0, q1);
-                    load_chunks<NCH>(klayer(kargs(), l + 1).attn_norm, nq);
-                }
             }
             // ---- o rows + residual
             if (wg_o)
@@ -772,12 +808,12 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                 stage_vector<H>(my_copy<H>(kargs().tx), tag_of(seq + 2), sm.vec, kargs().error_flag);
             stamp<S>(3 + 4 * l);
             stamp_wg(l, n_layers, 4);
+            if (wg_g) wg_rmsnorm<H>(sm.vec, ng, kargs().eps, &norm_inv);
             if (g0 < g1) {
                 KArgs &a = kargs();
                 KLayer &L = klayer(a, l);
-                u32x4 x[NCH], xb[NCH];
-                lds_chunks<NCH>(sm.vec, x);
-                wave_rmsnorm<NCH>(x, ng, a.eps, xb);
+                u32x4 xb[NCH];
+                lds_chunks<NCH>(sm.vec, xb);
                 uint32_t *hb = a.thb;
                 const uint32_t tag = tag_of(seq + 3);
                 wave_gemv2<NCH, S::B_GU>(L.w_gate, L.w_up, g0, g1, xb, pf_g, pf_u,
@@ -806,10 +842,9 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
             }
             stamp_wg(l, n_layers, 7);
             if constexpr (!S::PF_EARLY) {
-                if (q0 < q1 && l + 1 < n_layers) {
+                if (wg_q && l + 1 < n_layers) nq.load(klayer(kargs(), l + 1).attn_norm);
+                if (q0 < q1 && l + 1 < n_layers)
                     pf_qkv.load(qkv_row(klayer(kargs(), l + 1)), q0, q1);
-                    load_chunks<NCH>(klayer(kargs(), l + 1).attn_norm, nq);
-                }
             }
         }
     }
@@ -823,20 +858,18 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
         const bf16 *lm = kargs().lm_head;
         auto lm_row = [=](int r) { return lm + (size_t)r * H; };
         Rows<NCH, S::B_LM> batch;
-        u32x4 nf[NCH];  // final_norm chunks
-        if (r0 < r1) {
-            batch.load(lm_row, r0, r1);
-            load_chunks<NCH>(kargs().final_norm, nf);
-        }
+        NormW<H> nf;  // final_norm weights
+        nf.load(kargs().final_norm);
+        if (r0 < r1) batch.load(lm_row, r0, r1);
         stage_vector<H>(my_copy<H>(kargs().tx), tag_of(seq_end - 1), sm.vec, kargs().error_flag);
         stamp<S>(1 + 4 * n_layers);
+        wg_rmsnorm<H>(sm.vec, nf, kargs().eps, &norm_inv);
         float best = -__builtin_huge_valf();
         int bidx = INT_MAX;
         if (r0 < r1) {
             KArgs &a = kargs();
-            u32x4 x[NCH], xb[NCH];
-            lds_chunks<NCH>(sm.vec, x);
-            wave_rmsnorm<NCH>(x, nf, a.eps, xb);
+            u32x4 xb[NCH];
+            lds_chunks<NCH>(sm.vec, xb);
             bf16 *logits = a.logits;
             wave_gemv<NCH, S::B_LM, true>(lm_row, r0, r1, xb, batch,
                                           [&](int r, float y, uint32_t) {
