@@ -227,6 +227,8 @@ static StepArgs step_args(const Config *cfg, const Weights *w, RunState *s, int 
     a.tattn = a.tqkv + step_replica_stride(qd + 2 * kvd);
     a.thb = a.tattn + STEP_REPLICAS * step_replica_stride(qd);
     a.epoch = &ws->epoch;
+    a.token_word = &ws->token_word;
+    a.n_tokens = 1;
     a.final_ctr = &ws->final_ctr;
     a.amax_val = ws->amax_val;
     a.amax_idx = ws->amax_idx;
@@ -328,9 +330,9 @@ extern "C" int generate_greedy(const Config *cfg, const Weights *w, RunState *s,
         set_token_pos_kernel<<<1, 64, 0, s->stream>>>(s->next_token, s->pos, token, pos);
         set_token_pos_kernel<<<1, 64, 0, s->stream>>>(s->error_flag, s->pos_base, 0, pos);
         if (!LAUNCH_OK()) return -1;
-        const StepArgs a = step_args(cfg, w, s, 1);
-        for (int i = 0; i < n_steps; i++)
-            if (!step_kernel_launch(cfg, a, s->step_grid, s->stream)) return -1;
+        StepArgs a = step_args(cfg, w, s, 1);
+        a.n_tokens = n_steps;  // one launch decodes every token
+        if (!step_kernel_launch(cfg, a, s->step_grid, s->stream)) return -1;
         s->next_token_valid = 1;
         if (!HIP_OK(hipMemcpyAsync(out_tokens, s->token_out, (size_t)n_steps * 4,
                                    hipMemcpyDeviceToHost, s->stream)) ||

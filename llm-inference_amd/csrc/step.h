@@ -25,13 +25,15 @@ struct StepArgs {
     bf16 *logits, *key_cache, *value_cache;
     uint32_t *tx, *tqkv, *tattn, *thb;
     int *next_token, *pos, *token_out, *pos_base, *error_flag;
-    unsigned *epoch;      // phases completed over all launches (the tag base)
-    unsigned *final_ctr;  // workgroups done with the LM head
+    unsigned *epoch;      // tagged phases written over all launches (the tag base)
+    unsigned *final_ctr;  // workgroups done with the LM head (counts over a launch's tokens)
+    unsigned long long *token_word;  // the next token, tagged: (token << 32) | tag
     float *amax_val;      // per-workgroup argmax partials
     int *amax_idx;
     long long *trace;     // optional wall-clock stamps of one workgroup's phases
     float eps, scale;
     int n_layers, vocab, max_seq, token_capacity, advance;
+    int n_tokens;  // decode steps this launch runs (each feeds its argmax to the next)
     float inv_freq[64];
 };
 
@@ -40,7 +42,8 @@ struct StepArgs {
 struct StepWorkspace {
     unsigned epoch;
     unsigned final_ctr;
-    unsigned pad[62];
+    unsigned long long token_word;
+    unsigned pad[60];
     float amax_val[1024];
     int amax_idx[1024];
 };

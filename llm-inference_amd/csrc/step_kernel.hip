@@ -105,50 +105,56 @@ __device__ __forceinline__ const uint32_t *my_copy(const uint32_t *v) {
     return v + (blockIdx.x % STEP_REPLICAS) * (int)step_replica_stride(N);
 }
 
-// Polls the 64-bit words src(p) (two tagged elements each) for the pairs p = threadIdx.x +
-// THREADS*j < PAIRS until both tags equal `tag`, and writes the bf16 pairs to dst[p] (LDS). The
-// whole workgroup takes part; it syncs before (the previous contents of dst have been read)
-// and after. Bounded: on timeout, or once another wave has timed out, it sets the error flag
-// and goes on with what it read.
-template <int PAIRS, class Src>
+// Polls the 64-bit words src(p) (two tagged elements each) for pairs p < PAIRS until both tags
+// equal `tag`, and writes the bf16 pairs to dst[p] (LDS). With ONE_WAVE only wave 0 polls (pair
+// p = lane + 64 j): a wave with weight loads in flight would see the data only after them, since
+// vector loads complete in order, so the workgroups that prefetch weights leave polling to a
+// wave that has none. Otherwise every thread polls (p = threadIdx.x + THREADS j). The workgroup
+// syncs before (the previous contents of dst have been read) and after. Bounded: on timeout, or
+// once another wave has timed out, it sets the error flag and goes on with what it read.
+template <int PAIRS, bool ONE_WAVE, class Src>
 __device__ __forceinline__ void stage_pairs(Src src, uint32_t tag, uint32_t *dst, int *err) {
-    constexpr int P = (PAIRS + THREADS - 1) / THREADS;
+    constexpr int STEP = ONE_WAVE ? 64 : THREADS;
+    constexpr int P = (PAIRS + STEP - 1) / STEP;
     __syncthreads();
-    const int t0 = threadIdx.x;
-    uint64_t w[P];
-    long long spins = 0;
-    for (;;) {
-        bool fresh = true;
+    if (!ONE_WAVE || (tid_x() >> 6) == 0) {
+        const int t0 = ONE_WAVE ? (tid_x() & 63) : (int)threadIdx.x;
+        uint64_t w[P];
+        long long spins = 0;
+        for (;;) {
+            bool fresh = true;
+#pragma unroll
+            for (int j = 0; j < P; j++) {
+                const int p = t0 + STEP * j;
+                if (p < PAIRS) {
+                    w[j] = ld_coh64(src(p));
+                    fresh &= (uint32_t)(w[j] & 0xffffu) == tag &&
+                             (uint32_t)((w[j] >> 32) & 0xffffu) == tag;
+                }
+            }
+            if (fresh) break;
+            if ((++spins & 63) == 0 &&
+                (spins > SPIN_LIMIT || ld_coh_u32((const unsigned *)err))) {
+                __hip_atomic_store(gptr(err), 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
 #pragma unroll
         for (int j = 0; j < P; j++) {
-            const int p = t0 + THREADS * j;
-            if (p < PAIRS) {
-                w[j] = ld_coh64(src(p));
-                fresh &= (uint32_t)(w[j] & 0xffffu) == tag &&
-                         (uint32_t)((w[j] >> 32) & 0xffffu) == tag;
-            }
+            const int p = t0 + STEP * j;
+            if (p < PAIRS)
+                dst[p] = (uint32_t)((w[j] >> 16) & 0xffffu) | ((uint32_t)(w[j] >> 48) << 16);
         }
-        if (fresh) break;
-        if ((++spins & 63) == 0 && (spins > SPIN_LIMIT || ld_coh_u32((const unsigned *)err))) {
-            __hip_atomic_store(gptr(err), 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-    }
-#pragma unroll
-    for (int j = 0; j < P; j++) {
-        const int p = t0 + THREADS * j;
-        if (p < PAIRS)
-            dst[p] = (uint32_t)((w[j] >> 16) & 0xffffu) | ((uint32_t)(w[j] >> 48) << 16);
     }
     __syncthreads();
 }
 
 // Elements [0, N) of tagged vector v into LDS as plain bf16 (N even).
-template <int N>
+template <int N, bool ONE_WAVE>
 __device__ __forceinline__ void stage_vector(const uint32_t *v, uint32_t tag, uint32_t *dst,
                                              int *err) {
-    stage_pairs<N / 2>([=](int p) { return v + 2 * p; }, tag, dst, err);
+    stage_pairs<N / 2, ONE_WAVE>([=](int p) { return v + 2 * p; }, tag, dst, err);
 }
 
 // The embedding row as the first layer's input (read-only: nothing to wait for).
@@ -215,6 +221,10 @@ __device__ __forceinline__ void wg_rmsnorm(uint32_t *vec, const NormW<N> &nw, fl
 
 // B rows of NC chunks each, held in registers: lane l has chunk l + 64k of every row. `rowp`
 // maps a row index to its data, so a batch can straddle the q/k/v matrices.
+// Declare them value-initialised (`Rows<..> r{};`) inside loops: a batch loaded only on some
+// paths is otherwise carried from the previous iteration (in SSA form a variable declared in a
+// loop body is one value across iterations), which holds its registers through the whole
+// loop. The zero fill survives only on the paths that do not load.
 template <int NC, int B>
 struct Rows {
     u32x4 w[B][NC];
@@ -309,15 +319,16 @@ __device__ __forceinline__ void wave_gemv2(const bf16 *Wg, const bf16 *Wu, int r
 // staged) or 2 * phase + 1 (results stored); phase 0 is q/k/v (or a head's attention), then
 // o, gate/up, down.
 constexpr int TRACE_LAYER = 1;
+// Only the first token of a launch is traced (step 0).
 template <class S>
-__device__ __forceinline__ void stamp(int i) {
-    if (blockIdx.x == S::HQ && threadIdx.x == 0) {
+__device__ __forceinline__ void stamp(int i, int step) {
+    if (step == 0 && blockIdx.x == S::HQ && threadIdx.x == 0) {
         long long *trace = kargs().trace;
         if (trace) gptr(trace)[i] = wall_clock64();
     }
 }
-__device__ __forceinline__ void stamp_wg(int l, int n_layers, int k) {
-    if (l == TRACE_LAYER) {
+__device__ __forceinline__ void stamp_wg(int l, int n_layers, int k, int step) {
+    if (step == 0 && l == TRACE_LAYER) {
         long long *trace = kargs().trace;
         if (trace) {
             if (k & 1) __syncthreads();  // "stored": when every wave has issued its stores
@@ -354,6 +365,21 @@ struct AttnSmem {
     float out[D];                   // running sum over blocks
 };
 
+// One lane's 16 bytes of a KV-cache row. Rows written earlier in this launch (t >= pos0) were
+// stored by another workgroup, possibly on another XCD, so they are read coherently; older rows
+// come from earlier launches and stream non-temporally.
+__device__ __forceinline__ u32x4 ld_kv(const bf16 *p, int t, int pos0) {
+    if (t >= pos0) {
+        const uint64_t a = ld_coh64(p), b = ld_coh64((const char *)p + 8);
+        return u32x4{(uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32)};
+    }
+    return ld16_nt(p);
+}
+__device__ __forceinline__ void st_kv(bf16 *p, uint32_t v) {
+    __hip_atomic_store(gptr((uint16_t *)p), (uint16_t)v, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Position of key slot u of this lane in the scores round starting at `base`, and of value
 // slot (j, it) in the PV round starting at block c0 (16 lanes per position, 8 waves).
 __device__ __forceinline__ int key_slot(int base, int u) {
@@ -365,7 +391,7 @@ __device__ __forceinline__ int value_slot(int c0, int j, int it) {
 }
 
 template <class S>
-__device__ __forceinline__ void attention_prefetch(KArgs &a, KLayer &L, int h, int pos,
+__device__ __forceinline__ void attention_prefetch(KArgs &a, KLayer &L, int h, int pos, int pos0,
                                                    int layer, AttnPrefetch &p) {
     constexpr int D = 128, REP = S::HQ / S::HKV, KVD = S::HKV * D;
     const int g = h / REP, Lp = tid_x() & 15;
@@ -379,7 +405,7 @@ __device__ __forceinline__ void attention_prefetch(KArgs &a, KLayer &L, int h, i
 #pragma unroll
     for (int u = 0; u < SCORE_LOADS; u++) {
         const int t = key_slot(0, u);
-        p.k[u] = t < pos ? ld16_nt(kc + (size_t)t * KVD) : u32x4{0, 0, 0, 0};
+        p.k[u] = t < pos ? ld_kv(kc + (size_t)t * KVD, t, pos0) : u32x4{0, 0, 0, 0};
     }
     rope_table<D>(pos, a.inv_freq, p.cs, p.sn);
     // computed here, before the workgroup waits for its q/k/v, not sunk to the first use
@@ -392,10 +418,10 @@ __device__ __forceinline__ void attention_prefetch(KArgs &a, KLayer &L, int h, i
 // then scores, block statistics, the global max/sum, probabilities, PV per 64-position block in
 // four quarters, and the in-order combine; the head's output is published with `tag_out`.
 template <class S>
-__device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int pos, int layer,
-                                               AttnSmem<S> &sm, AttnPrefetch &pre,
-                                               uint32_t tag_in, uint32_t tag_out,
-                                               int n_layers) {
+__device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int pos, int pos0,
+                                               int layer, AttnSmem<S> &sm, AttnPrefetch &pre,
+                                               uint32_t tag_in, uint32_t tag_out, int n_layers,
+                                               int step) {
     constexpr int D = 128, REP = S::HQ / S::HKV, QD = S::HQ * D, KVD = S::HKV * D;
     const int lane = tid_x() & 63, w = tid_x() >> 6;
     const int g = h / REP;
@@ -409,14 +435,14 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
     {
         const uint32_t *qkv = a.tqkv;
         const int qo = h * D, ko = QD + g * D, vo = QD + KVD + g * D;
-        stage_pairs<3 * D / 2>(
+        stage_pairs<3 * D / 2, false>(
             [=](int p) {
                 const int seg = p / (D / 2), i = 2 * (p % (D / 2));
                 return qkv + (seg == 0 ? qo : seg == 1 ? ko : vo) + i;
             },
             tag_in, &sm.raw[0][0], a.error_flag);
     }
-    stamp_wg(layer, n_layers, 0);
+    stamp_wg(layer, n_layers, 0, step);
 
     // history values of a PV round; the first round is requested now and lands during the
     // prologue, the scores and the softmax
@@ -428,7 +454,7 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
 #pragma unroll
             for (int it = 0; it < 4; it++) {
                 const int t = value_slot(c0, j, it);
-                vv[j][it] = t < pos ? ld16_nt(vc + (size_t)t * KVD + g * D + 8 * Lq) : zero;
+                vv[j][it] = t < pos ? ld_kv(vc + (size_t)t * KVD + g * D + 8 * Lq, t, pos0) : zero;
             }
     };
     load_v(0);
@@ -469,16 +495,16 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
             dst[lane] = (uint16_t)oa;
             dst[64 + lane] = (uint16_t)ob;
             if (w == 1 && owner) {
-                gptr((uint16_t *)(kc + row))[lane] = (uint16_t)oa;
-                gptr((uint16_t *)(kc + row))[64 + lane] = (uint16_t)ob;
+                st_kv(kc + row + lane, oa);
+                st_kv(kc + row + 64 + lane, ob);
             }
         } else {
             uint16_t *dst = (uint16_t *)sm.v;
             dst[lane] = (uint16_t)xi;
             dst[64 + lane] = (uint16_t)xj;
             if (owner) {
-                gptr((uint16_t *)(vc + row))[lane] = (uint16_t)xi;
-                gptr((uint16_t *)(vc + row))[64 + lane] = (uint16_t)xj;
+                st_kv(vc + row + lane, xi);
+                st_kv(vc + row + 64 + lane, xj);
             }
         }
     }
@@ -495,7 +521,7 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
             for (int u = 0; u < SCORE_LOADS; u++) {
                 const int t = key_slot(base, u);
                 if (base == 0) kv[u] = t == pos ? kcur : pre.k[u];
-                else kv[u] = t < pos ? ld16_nt(kc + (size_t)t * KVD + g * D + 8 * Lp)
+                else kv[u] = t < pos ? ld_kv(kc + (size_t)t * KVD + g * D + 8 * Lp, t, pos0)
                                      : (t == pos ? kcur : zero);
             }
 #pragma unroll
@@ -622,28 +648,37 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
         }
         __syncthreads();
     }
+    // the KV row this workgroup stored is complete before the output that later steps depend
+    // on is published (a later token of the launch reads it from another workgroup)
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
     if (threadIdx.x < D)
         put_tagged_all<QD>(a.tattn, h * D + threadIdx.x, f2bf(sm.out[threadIdx.x]), tag_out);
 }
 
 // ---------------------------------------------------------------- the step
 
-// Rows [r0, r1) of a phase with R rows owned by wave w of this workgroup, the rows spread over
-// the waves of workgroups first_wg.. in order (so a workgroup owns rows iff its wave 0 does).
+// Rows [r0, r1) of a phase with R rows owned by wave w of this workgroup, the rows spread in
+// order over waves FIRST_W..7 of workgroups first_wg.. (so a workgroup owns rows iff its wave
+// FIRST_W does). Waves below FIRST_W own none.
+template <int FIRST_W>
 __device__ __forceinline__ void phase_rows(int R, int first_wg, int w, int &r0, int &r1) {
-    const int nw = ((int)gridDim.x - first_wg) * WAVES;
+    constexpr int RW = WAVES - FIRST_W;
+    const int nw = ((int)gridDim.x - first_wg) * RW;
     const int per = (R + nw - 1) / nw;
-    const int gw = ((int)blockIdx.x - first_wg) * WAVES + w;
-    const bool none = (int)blockIdx.x < first_wg;
+    const int gw = ((int)blockIdx.x - first_wg) * RW + w - FIRST_W;
+    const bool none = (int)blockIdx.x < first_wg || w < FIRST_W;
     r0 = none ? R : min(R, gw * per);
     r1 = none ? R : min(R, r0 + per);
 }
+template <int FIRST_W>
 __device__ __forceinline__ void phase_rows(int R, int first_wg, int &r0, int &r1) {
-    phase_rows(R, first_wg, __builtin_amdgcn_readfirstlane(tid_x() >> 6), r0, r1);
+    phase_rows<FIRST_W>(R, first_wg, __builtin_amdgcn_readfirstlane(tid_x() >> 6), r0, r1);
 }
+template <int FIRST_W>
 __device__ __forceinline__ bool workgroup_has_rows(int R, int first_wg) {
     int r0, r1;
-    phase_rows(R, first_wg, 0, r0, r1);
+    phase_rows<FIRST_W>(R, first_wg, FIRST_W, r0, r1);
     return r0 < r1;
 }
 
@@ -661,7 +696,7 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
     __shared__ int last_wg;
     __shared__ float norm_inv;
 
-    int token, pos, n_layers;
+    int token, pos, n_layers, n_tokens;
     unsigned seq0;  // tagged phases before this launch
     {
         KArgs &a = kargs();
@@ -669,12 +704,15 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
         token = *gptr(a.next_token);
         pos = *gptr(a.pos);
         n_layers = a.n_layers;
-        if (pos < 0 || pos >= a.max_seq || token < 0 || token >= a.vocab) {
+        n_tokens = a.n_tokens;
+        if (pos < 0 || n_tokens < 1 || pos + n_tokens > a.max_seq || token < 0 ||
+            token >= a.vocab) {
             if (blockIdx.x == 0 && threadIdx.x == 0) *gptr(a.error_flag) = 1;
             return;  // every workgroup reads the same values and leaves at once
         }
     }
-    stamp<S>(0);
+    const int pos0 = pos;  // KV rows from pos0 on are written during this launch
+    const unsigned seq_step = PHASES * n_layers + 1;  // tags per token: 5 per layer + the token
 
     // Workgroups 0..HQ-1 run one query head's attention each and own no matrix rows; the
     // others own the matrix rows and, while attention runs, load the weights of the o,
@@ -684,12 +722,14 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
     // what every later writer of that vector waits for, so it never sees a value overwritten.
     const bool attn_wg = (int)blockIdx.x < S::HQ;
     int q0, q1, o0, o1, g0, g1;
-    phase_rows(QD + 2 * KVD, S::HQ, q0, q1);
-    phase_rows(H, S::HQ, o0, o1);
-    phase_rows(I, S::HQ, g0, g1);
-    const bool wg_q = workgroup_has_rows(QD + 2 * KVD, S::HQ);
-    const bool wg_o = workgroup_has_rows(H, S::HQ);
-    const bool wg_g = workgroup_has_rows(I, S::HQ);
+    constexpr int FW = S::POLLER ? 1 : 0;  // first wave with matrix rows
+    constexpr bool OW = S::POLLER;         // staging by wave 0 alone
+    phase_rows<FW>(QD + 2 * KVD, S::HQ, q0, q1);
+    phase_rows<FW>(H, S::HQ, o0, o1);
+    phase_rows<FW>(I, S::HQ, g0, g1);
+    const bool wg_q = workgroup_has_rows<FW>(QD + 2 * KVD, S::HQ);
+    const bool wg_o = workgroup_has_rows<FW>(H, S::HQ);
+    const bool wg_g = workgroup_has_rows<FW>(I, S::HQ);
 
     auto qkv_row = [](KLayer &L) {
         const bf16 *wq = L.wq, *wk = L.wk, *wv = L.wv;
@@ -714,19 +754,22 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
         };
     };
 
+    for (int step = 0; step < n_tokens; step++, pos++) {
+    const unsigned sq0 = seq0 + step * seq_step;  // this token's first tag
+    stamp<S>(0, step);
     // tags of layer l: seq q|k|v, seq+1 attention, seq+2 x after o, seq+3 SwiGLU, seq+4 x
-    // after down, with seq = seq0 + PHASES * l
+    // after down, with seq = sq0 + PHASES * l; the next token: sq0 + PHASES * n_layers
     if (attn_wg) {
         // ---- QK-norm + RoPE + KV write + attention, one query head per workgroup
         for (int l = 0; l < n_layers; l++) {
-            const unsigned seq = seq0 + PHASES * l;
+            const unsigned seq = sq0 + PHASES * l;
             for (int h = blockIdx.x; h < S::HQ; h += gridDim.x) {
                 KArgs &a = kargs();
                 AttnPrefetch pre;
-                attention_prefetch<S>(a, klayer(a, l), h, opaque(pos), l, pre);
-                attention_head<S>(a, klayer(a, l), h, opaque(pos), l, sm.attn, pre,
-                                  tag_of(seq), tag_of(seq + 1), n_layers);
-                stamp_wg(l, n_layers, 1);
+                attention_prefetch<S>(a, klayer(a, l), h, opaque(pos), opaque(pos0), l, pre);
+                attention_head<S>(a, klayer(a, l), h, opaque(pos), opaque(pos0), l, sm.attn, pre,
+                                  tag_of(seq), tag_of(seq + 1), n_layers, step);
+                stamp_wg(l, n_layers, 1, step);
             }
         }
     } else {
@@ -737,23 +780,23 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
             const uint16_t *erow = (const uint16_t *)(kargs().embed + (size_t)token * H);
             xown = o0 + lane < o1 ? (uint32_t)gptr(erow)[o0 + lane] : 0u;
         }
-        Rows<NCH, S::B_QKV> pf_qkv;
-        NormW<H> nq;  // attn_norm weights of the coming q/k/v phase
+        Rows<NCH, S::B_QKV> pf_qkv{};
+        NormW<H> nq{};  // attn_norm weights of the coming q/k/v phase
         if (wg_q) nq.load(klayer(kargs(), 0).attn_norm);
         if (q0 < q1) pf_qkv.load(qkv_row(klayer(kargs(), 0)), q0, q1);
         for (int l = 0; l < n_layers; l++) {
-            const unsigned seq = seq0 + PHASES * l;
+            const unsigned seq = sq0 + PHASES * l;
             // ---- rmsnorm + q/k/v rows (weights requested a phase ahead)
             if (wg_q) {
                 if (l == 0) {
                     stage_plain<H>(kargs().embed + (size_t)token * H, sm.vec);
                 } else {
-                    stage_vector<H>(my_copy<H>(kargs().tx), tag_of(seq - 1), sm.vec,
-                                    kargs().error_flag);
+                    stage_vector<H, OW>(my_copy<H>(kargs().tx), tag_of(seq - 1), sm.vec,
+                                        kargs().error_flag);
                 }
             }
-            stamp<S>(1 + 4 * l);
-            stamp_wg(l, n_layers, 0);
+            stamp<S>(1 + 4 * l, step);
+            stamp_wg(l, n_layers, 0, step);
             if (wg_q) wg_rmsnorm<H>(sm.vec, nq, kargs().eps, &norm_inv);
             if (q0 < q1) {
                 KArgs &a = kargs();
@@ -769,12 +812,12 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                                                     return b;
                                                 });
             }
-            stamp_wg(l, n_layers, 1);
+            stamp_wg(l, n_layers, 1, step);
             // weights of the next phases, loaded while attention runs
-            Rows<NCO, S::B_O> pf_o;
-            Rows<NCH, S::B_GU> pf_g, pf_u;
-            Rows<NCI, S::B_DOWN> pf_d;
-            NormW<H> ng;  // mlp_norm weights
+            Rows<NCO, S::B_O> pf_o{};
+            Rows<NCH, S::B_GU> pf_g{}, pf_u{};
+            Rows<NCI, S::B_DOWN> pf_d{};
+            NormW<H> ng{};  // mlp_norm weights
             if (o0 < o1) pf_o.load(o_row(klayer(kargs(), l)), o0, o1);
             if (wg_g) ng.load(klayer(kargs(), l).mlp_norm);
             if (g0 < g1) {
@@ -791,10 +834,10 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
             }
             // ---- o rows + residual
             if (wg_o)
-                stage_vector<QD>(my_copy<QD>(kargs().tattn), tag_of(seq + 1), sm.vec,
-                                 kargs().error_flag);
-            stamp<S>(2 + 4 * l);
-            stamp_wg(l, n_layers, 2);
+                stage_vector<QD, OW>(my_copy<QD>(kargs().tattn), tag_of(seq + 1), sm.vec,
+                                     kargs().error_flag);
+            stamp<S>(2 + 4 * l, step);
+            stamp_wg(l, n_layers, 2, step);
             if (o0 < o1) {
                 u32x4 in[NCO];
                 lds_chunks<NCO>(sm.vec, in);
@@ -802,12 +845,13 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                                                           pf_o, residual(kargs().tx, tag_of(seq + 2)),
                                                           &xown);
             }
-            stamp_wg(l, n_layers, 3);
+            stamp_wg(l, n_layers, 3, step);
             // ---- rmsnorm + gate/up rows + SwiGLU
             if (wg_g)
-                stage_vector<H>(my_copy<H>(kargs().tx), tag_of(seq + 2), sm.vec, kargs().error_flag);
-            stamp<S>(3 + 4 * l);
-            stamp_wg(l, n_layers, 4);
+                stage_vector<H, OW>(my_copy<H>(kargs().tx), tag_of(seq + 2), sm.vec,
+                                    kargs().error_flag);
+            stamp<S>(3 + 4 * l, step);
+            stamp_wg(l, n_layers, 4, step);
             if (wg_g) wg_rmsnorm<H>(sm.vec, ng, kargs().eps, &norm_inv);
             if (g0 < g1) {
                 KArgs &a = kargs();
@@ -823,15 +867,16 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                     put_tagged_all<I>(hb, r, f2bf(s * bf2f(ub)), tag);
                 });
             }
-            stamp_wg(l, n_layers, 5);
+            stamp_wg(l, n_layers, 5, step);
             if constexpr (!S::PF_EARLY) {
                 if (o0 < o1) pf_d.load(d_row(klayer(kargs(), l)), o0, o1);
             }
             // ---- down rows + residual
             if (wg_o)
-                stage_vector<I>(my_copy<I>(kargs().thb), tag_of(seq + 3), sm.vec, kargs().error_flag);
-            stamp<S>(4 + 4 * l);
-            stamp_wg(l, n_layers, 6);
+                stage_vector<I, OW>(my_copy<I>(kargs().thb), tag_of(seq + 3), sm.vec,
+                                    kargs().error_flag);
+            stamp<S>(4 + 4 * l, step);
+            stamp_wg(l, n_layers, 6, step);
             if (o0 < o1) {
                 u32x4 in[NCI];
                 lds_chunks<NCI>(sm.vec, in);
@@ -840,7 +885,7 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                                                              residual(kargs().tx, tag_of(seq + 4)),
                                                              &xown);
             }
-            stamp_wg(l, n_layers, 7);
+            stamp_wg(l, n_layers, 7, step);
             if constexpr (!S::PF_EARLY) {
                 if (wg_q && l + 1 < n_layers) nq.load(klayer(kargs(), l + 1).attn_norm);
                 if (q0 < q1 && l + 1 < n_layers)
@@ -852,17 +897,18 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
     // ---- final rmsnorm + LM head + argmax over every workgroup (two batches of LM-head rows
     // in flight; the first is requested before the residual stream is polled)
     {
-        const unsigned seq_end = seq0 + PHASES * n_layers;
+        const unsigned seq_end = sq0 + PHASES * n_layers;  // the next token's tag
         int r0, r1;
-        phase_rows(kargs().vocab, 0, r0, r1);
+        phase_rows<FW>(kargs().vocab, 0, r0, r1);
         const bf16 *lm = kargs().lm_head;
         auto lm_row = [=](int r) { return lm + (size_t)r * H; };
-        Rows<NCH, S::B_LM> batch;
-        NormW<H> nf;  // final_norm weights
+        Rows<NCH, S::B_LM> batch{};
+        NormW<H> nf{};  // final_norm weights
         nf.load(kargs().final_norm);
         if (r0 < r1) batch.load(lm_row, r0, r1);
-        stage_vector<H>(my_copy<H>(kargs().tx), tag_of(seq_end - 1), sm.vec, kargs().error_flag);
-        stamp<S>(1 + 4 * n_layers);
+        stage_vector<H, OW>(my_copy<H>(kargs().tx), tag_of(seq_end - 1), sm.vec,
+                            kargs().error_flag);
+        stamp<S>(1 + 4 * n_layers, step);
         wg_rmsnorm<H>(sm.vec, nf, kargs().eps, &norm_inv);
         float best = -__builtin_huge_valf();
         int bidx = INT_MAX;
@@ -894,9 +940,10 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
             __hip_atomic_store(gptr(&a.amax_idx[blockIdx.x]), bidx, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
             __builtin_amdgcn_s_waitcnt(0);
+            // the counter runs over the launch's tokens: step s ends at (s + 1) * grid arrivals
             const unsigned done = __hip_atomic_fetch_add(gptr(a.final_ctr), 1u, __ATOMIC_RELAXED,
                                                          __HIP_MEMORY_SCOPE_AGENT);
-            last_wg = done == gridDim.x - 1;
+            last_wg = done == (unsigned)(step + 1) * gridDim.x - 1;
         }
         __syncthreads();
         if (last_wg && w == 0) {
@@ -919,11 +966,44 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                     if (i >= 0 && i < a.token_capacity) gptr(a.token_out)[i] = idx;
                     *gptr(a.pos) = pos + 1;
                 }
-                *gptr(a.final_ctr) = 0;
-                *gptr(a.epoch) = seq_end;
-                if (a.trace) gptr(a.trace)[2 + 4 * n_layers] = wall_clock64();
+                if (step + 1 < n_tokens) {
+                    // the next token for every workgroup
+                    __hip_atomic_store(gptr(a.token_word),
+                                       ((unsigned long long)(unsigned)idx << 32) | tag_of(seq_end),
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                } else {
+                    *gptr(a.final_ctr) = 0;
+                    *gptr(a.epoch) = seq0 + n_tokens * seq_step;
+                    if (a.trace) gptr(a.trace)[2 + 4 * n_layers] = wall_clock64();
+                }
             }
         }
+        if (step + 1 < n_tokens) {
+            // wait for the token this step chose (bounded like every other wait)
+            __shared__ int next_tok;
+            if (threadIdx.x == 0) {
+                KArgs &a = kargs();
+                unsigned long long tw = 0;
+                long long spins = 0;
+                for (;;) {
+                    tw = __hip_atomic_load(gptr(a.token_word), __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                    if ((uint32_t)tw == tag_of(seq_end)) break;
+                    if ((++spins & 63) == 0 &&
+                        (spins > SPIN_LIMIT || ld_coh_u32((const unsigned *)a.error_flag))) {
+                        __hip_atomic_store(gptr(a.error_flag), 2, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+                const int t = (int)(tw >> 32);
+                next_tok = t >= 0 && t < a.vocab ? t : 0;
+            }
+            __syncthreads();
+            token = next_tok;
+        }
+    }
     }
 }
 
@@ -946,6 +1026,9 @@ struct Shape {
     static constexpr int B_DOWN = 1;
     static constexpr int B_LM = H <= 1024 ? 8 : (H <= 2048 ? 4 : 2);
     static constexpr bool PF_EARLY = H <= 1024;
+    // wave 0 of every workgroup stages the vectors and owns no matrix rows (so no weight load
+    // is in flight in the polling wave); the larger shapes' vectors need every wave to poll
+    static constexpr bool POLLER = false;
     static constexpr bool O_STREAM = H > 1024;
     static constexpr bool D_STREAM = H > 1024;
 };
@@ -967,10 +1050,10 @@ static const void *step_kernel_for(const Config *c) {
 }
 
 // The kernel's layout needs workgroups beyond the attention ones (at least as many again) and
-// at most 64 residual rows per matrix wave.
+// at most 64 residual rows per matrix wave (7 matrix waves per workgroup when wave 0 polls).
 static bool step_grid_fits(const Config *c, int grid) {
     if (grid <= 0 || grid > 1024 || grid < 2 * c->n_heads) return false;
-    const int waves = (grid - c->n_heads) * WAVES;
+    const int waves = (grid - c->n_heads) * (WAVES - 1);
     return (c->hidden_size + waves - 1) / waves <= 64;
 }
 

@@ -273,6 +273,47 @@ def test_persistent_step_logits_per_position(gpu, oracle):
         dec.close()
 
 
+def test_persistent_generate_one_launch_small(gpu, oracle):
+    """generate_greedy in persistent mode decodes every token in ONE launch (each token's argmax
+    feeds the next inside the kernel; KV rows written earlier in the launch are read back by the
+    other heads of the group). 150 tokens on the smallest specialised shapes cross the 64- and
+    128-position block edges: tokens equal the oracle's and per-token persistent launches'."""
+    ident("persistent one-launch generate small shapes")
+    from llm_inference_amd import model
+    cfg = model.make_config(hidden_size=512, intermediate_size=1024, n_layers=3, n_heads=8,
+                            n_kv_heads=4, vocab_size=5000, max_seq_len=200)
+    dec = model.Decoder(cfg, ("synth", 4, 0.02, 0.1))
+    try:
+        w = dec.host_weights()
+        prompt = [17, 4000, 250, 3]
+        dec.capture_graph("persistent")
+        for pos, tok in enumerate(prompt):
+            dec.forward(tok, pos)
+        first = dec.sample_argmax()
+        got = dec.generate_greedy(first, len(prompt), 150)
+        t, per = first, []
+        for i in range(150):
+            dec.forward(t, len(prompt) + i)
+            t = dec.sample_argmax()
+            per.append(t)
+        assert got == per
+        orc = oracle.Model(oracle_cfg(cfg), w, max_seq=200)
+        for pos, tok in enumerate(prompt):
+            t = orc.forward(tok, pos, oracle.GPU_ORDER)
+        ref = []
+        for i in range(150):
+            t = orc.forward(t, len(prompt) + i, oracle.GPU_ORDER)
+            ref.append(t)
+        assert got == ref
+        # a second call continues from the state the first left
+        more = dec.generate_greedy(got[-1], len(prompt) + 150, 20)
+        for i in range(20):
+            t = orc.forward(t, len(prompt) + 150 + i, oracle.GPU_ORDER)
+            assert more[i] == t, i
+    finally:
+        dec.close()
+
+
 def test_persistent_step_long_context(qwen06b, oracle):
     """One decode position at 5000 with the KV cache below it filled with N(0, 1): the
     persistent step's attention over 79 blocks of 64 positions is bit-identical to the
