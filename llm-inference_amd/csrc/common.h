@@ -35,6 +35,12 @@ __device__ __forceinline__ u32x4 ld16_nt(const void *p) {
 }
 __device__ __forceinline__ void st16(void *p, u32x4 v) { *gptr((u32x4 *)p) = v; }
 
+// Word 3 of a raw buffer descriptor (CDNA): 32-bit data format, no swizzle, no stride; loads at
+// offsets past the descriptor's size return zero without a memory access.
+constexpr int BUFFER_FLAGS = 0x00020000;
+// Cache policy operand of a buffer load: non-temporal, as ld16_nt.
+constexpr int BUFFER_NT = 2;
+
 // bf16 element e of a packed 16-byte chunk (element 0 in the low half of dword 0).
 __device__ __forceinline__ float lo_f(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_f(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
@@ -116,11 +122,13 @@ __device__ __forceinline__ float group_sum(float v) {
 }
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
 
-template <int S>
+template <int S, int N = 64>
 __device__ __forceinline__ float butterfly_max(float v) {
-    if constexpr (S < 64) return butterfly_max<2 * S>(fmaxf(v, xor_lane<S>(v)));
+    if constexpr (S < N) return butterfly_max<2 * S, N>(fmaxf(v, xor_lane<S>(v)));
     else return v;
 }
+template <int N>
+__device__ __forceinline__ float group_max(float v) { return butterfly_max<1, N>(v); }
 __device__ __forceinline__ float wave_max(float v) { return butterfly_max<1>(v); }
 
 // Wave sums of B rows (B a power of two up to 64) with the pairing of wave_sum, so each total
@@ -136,10 +144,10 @@ __device__ __forceinline__ int scatter_row(int lane) {
         if ((lane >> k) & 1) row += B >> (k + 1);
     return row;
 }
-template <int M, int S>
+template <int M, int S, int N = 64>
 __device__ __forceinline__ float scatter_sum_step(const float *v) {
     if constexpr (M == 1) {
-        return butterfly_sum<S, 64>(v[0]);
+        return butterfly_sum<S, N>(v[0]);
     } else {
         const bool up = (tid_x() & S) != 0;
         float keep[M / 2];
@@ -149,13 +157,20 @@ __device__ __forceinline__ float scatter_sum_step(const float *v) {
             const float recv = xor_lane<S>(up ? lo : hi);
             keep[j] = (up ? hi : lo) + recv;
         }
-        return scatter_sum_step<M / 2, 2 * S>(keep);
+        return scatter_sum_step<M / 2, 2 * S, N>(keep);
     }
 }
 template <int B>
 __device__ __forceinline__ float wave_sum_scatter(const float (&v)[B]) {
     static_assert(B >= 1 && B <= 64 && (B & (B - 1)) == 0, "rows per batch");
     return scatter_sum_step<B, 1>(v);
+}
+// The same over aligned groups of N lanes: each total is bit-identical to group_sum<N> of that
+// row, and lane l ends with row scatter_row<B>(l) (B <= N).
+template <int N, int B>
+__device__ __forceinline__ float group_sum_scatter(const float (&v)[B]) {
+    static_assert(B >= 1 && B <= N && N <= 64 && (B & (B - 1)) == 0, "rows per group");
+    return scatter_sum_step<B, 1, N>(v);
 }
 
 // Larger value wins, equal values keep the lower index; NaN is never taken.

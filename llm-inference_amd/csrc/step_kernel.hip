@@ -180,15 +180,19 @@ __device__ __forceinline__ void lds_chunks(const uint32_t *vec, u32x4 (&out)[NC]
 template <int N>
 struct NormW {
     static constexpr int E = (N + THREADS - 1) / THREADS;
-    float w[E];
+    // the raw bf16 bits, widened where they are used: converting at the load would make the
+    // wave wait for this load, and with it for every weight request issued before it
+    uint32_t w[E];
     __device__ __forceinline__ void load(const bf16 *g) {
         const uint16_t *g16 = (const uint16_t *)g;
 #pragma unroll
         for (int j = 0; j < E; j++) {
             const int i = threadIdx.x + THREADS * j;
-            w[j] = i < N ? bf2f(gptr(g16)[i]) : 0.0f;
+            if constexpr (N % THREADS == 0) w[j] = gptr(g16)[i];
+            else w[j] = i < N ? (uint32_t)gptr(g16)[i] : 0u;
         }
     }
+    __device__ __forceinline__ float operator[](int j) const { return bf2f((bf16)w[j]); }
 };
 
 // RMSNorm of the staged vector (LDS, bf16), in place, once per workgroup with the arithmetic of
@@ -214,7 +218,7 @@ __device__ __forceinline__ void wg_rmsnorm(uint32_t *vec, const NormW<N> &nw, fl
 #pragma unroll
     for (int j = 0; j < NormW<N>::E; j++) {
         const int i = threadIdx.x + THREADS * j;
-        if (i < N) v16[i] = (uint16_t)f2bf(round_bf(bf2f((bf16)v16[i]) * inv) * nw.w[j]);
+        if (i < N) v16[i] = (uint16_t)f2bf(round_bf(bf2f((bf16)v16[i]) * inv) * nw[j]);
     }
     __syncthreads();
 }
@@ -228,14 +232,23 @@ __device__ __forceinline__ void wg_rmsnorm(uint32_t *vec, const NormW<N> &nw, fl
 template <int NC, int B>
 struct Rows {
     u32x4 w[B][NC];
+    // Rows at or past r1 (a short last batch, or a wave without rows: r = r1) read as zeros
+    // with no memory access: each row is a buffer whose size is zero when the row is absent,
+    // and buffer loads past the end return 0. The request is thus made on every path, with no
+    // branch around it (see the step kernel).
     template <class RowP>
     __device__ __forceinline__ void load(RowP rowp, int r, int r1) {
         const int lane = tid_x() & 63;
 #pragma unroll
         for (int i = 0; i < B; i++) {
-            const bf16 *row = rowp(min(r + i, r1 - 1));
+            const bool in = r + i < r1;
+            const bf16 *row = rowp(in ? r + i : 0);
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                (void *)row, (short)0, in ? NC * 1024 : 0, BUFFER_FLAGS);
 #pragma unroll
-            for (int k = 0; k < NC; k++) w[i][k] = ld16_nt(row + 8 * (lane + 64 * k));
+            for (int k = 0; k < NC; k++)
+                w[i][k] = __builtin_amdgcn_raw_buffer_load_b128(rs, 16 * (lane + 64 * k), 0,
+                                                                BUFFER_NT);
         }
     }
 };
@@ -288,8 +301,12 @@ __device__ __forceinline__ void wave_gemv(RowP rowp, int r0, int r1, const u32x4
             finish(batch_sums(nxt, xin), r + B);
         }
     } else {
-        for (int r = r0; r < r1; r += B) {
-            if (r != r0) cur.load(rowp, r, r1);
+        // the first batch outside the loop: a loop head would merge this batch's (long
+        // complete) registers with the loads of the loop's back edge, and the wait placed there
+        // would then also wait for every request issued since the prefetch
+        if (r0 < r1) finish(batch_sums(cur, xin), r0);
+        for (int r = r0 + B; r < r1; r += B) {
+            cur.load(rowp, r, r1);
             finish(batch_sums(cur, xin), r);
         }
     }
@@ -302,14 +319,16 @@ __device__ __forceinline__ void wave_gemv2(const bf16 *Wg, const bf16 *Wu, int r
                                            Rows<NC, B> &ub, Epi epi) {
     const int lane = tid_x() & 63;
     constexpr int COLS = 512 * NC;
-    for (int r = r0; r < r1; r += B) {
-        if (r != r0) {
-            gb.load([&](int rr) { return Wg + (size_t)rr * COLS; }, r, r1);
-            ub.load([&](int rr) { return Wu + (size_t)rr * COLS; }, r, r1);
-        }
+    auto finish = [&](int r) {
         const float tg = batch_sums(gb, xin), tu = batch_sums(ub, xin);
         const int row = r + scatter_row<B>(lane);
         if (lane < B && row < r1) epi(row, tg, tu);
+    };
+    if (r0 < r1) finish(r0);  // outside the loop, as in wave_gemv
+    for (int r = r0 + B; r < r1; r += B) {
+        gb.load([&](int rr) { return Wg + (size_t)rr * COLS; }, r, r1);
+        ub.load([&](int rr) { return Wu + (size_t)rr * COLS; }, r, r1);
+        finish(r);
     }
 }
 
@@ -342,13 +361,15 @@ __device__ __forceinline__ void stamp_wg(int l, int n_layers, int k, int step) {
 constexpr int PV_ROUND = 4;     // 64-position blocks per PV round (two per wave)
 constexpr int SCORE_LOADS = 8;  // keys per lane per scores round (8 * 4 * WAVES positions)
 
-// History keys (positions < pos, written by earlier steps) of the first scores round of one
-// head, requested before its q/k/v are polled, and this lane's RoPE table entry at pos. Key
-// slots at or beyond pos hold zeros; attention_head substitutes the current position's key.
+// History keys and values (positions < pos, written by earlier steps) of the first scores and
+// PV rounds of one head, requested before its q/k/v are polled, and this lane's RoPE table entry
+// at pos. Slots at or beyond pos hold zeros; attention_head substitutes the current position's
+// key and value.
 struct AttnPrefetch {
     u32x4 k[SCORE_LOADS];
+    u32x4 v[PV_ROUND / 2][4];
     float cs[1], sn[1];  // RoPE table entry `lane` (rotation pair lane, lane + 64)
-    float w0, w1;        // waves 0/1: q/k norm weights of elements lane and lane + 64
+    uint32_t w0, w1;     // waves 0/1: q/k norm weights (bf16 bits) of elements lane, lane + 64
 };
 
 template <class S>
@@ -398,8 +419,8 @@ __device__ __forceinline__ void attention_prefetch(KArgs &a, KLayer &L, int h, i
     {
         const int lane = tid_x() & 63;
         const uint16_t *nw = (const uint16_t *)((tid_x() >> 6) == 1 ? L.k_norm : L.q_norm);
-        p.w0 = bf2f(gptr(nw)[lane]);
-        p.w1 = bf2f(gptr(nw)[64 + lane]);
+        p.w0 = gptr(nw)[lane];
+        p.w1 = gptr(nw)[64 + lane];
     }
     const bf16 *kc = a.key_cache + (size_t)layer * a.max_seq * KVD + g * D + 8 * Lp;
 #pragma unroll
@@ -407,6 +428,14 @@ __device__ __forceinline__ void attention_prefetch(KArgs &a, KLayer &L, int h, i
         const int t = key_slot(0, u);
         p.k[u] = t < pos ? ld_kv(kc + (size_t)t * KVD, t, pos0) : u32x4{0, 0, 0, 0};
     }
+    const bf16 *vc = a.value_cache + (size_t)layer * a.max_seq * KVD + g * D + 8 * Lp;
+#pragma unroll
+    for (int j = 0; j < PV_ROUND / 2; j++)
+#pragma unroll
+        for (int it = 0; it < 4; it++) {
+            const int t = value_slot(0, j, it);
+            p.v[j][it] = t < pos ? ld_kv(vc + (size_t)t * KVD, t, pos0) : u32x4{0, 0, 0, 0};
+        }
     rope_table<D>(pos, a.inv_freq, p.cs, p.sn);
     // computed here, before the workgroup waits for its q/k/v, not sunk to the first use
     asm volatile("" : "+v"(p.cs[0]), "+v"(p.sn[0]));
@@ -444,9 +473,12 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
     }
     stamp_wg(layer, n_layers, 0, step);
 
-    // history values of a PV round; the first round is requested now and lands during the
-    // prologue, the scores and the softmax
+    // history values of a PV round (the first one prefetched)
     u32x4 vv[PV_ROUND / 2][4];
+#pragma unroll
+    for (int j = 0; j < PV_ROUND / 2; j++)
+#pragma unroll
+        for (int it = 0; it < 4; it++) vv[j][it] = pre.v[j][it];
     auto load_v = [&](int c0) {
         const int Lq = tid_x() & 15;
 #pragma unroll
@@ -457,7 +489,6 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
                 vv[j][it] = t < pos ? ld_kv(vc + (size_t)t * KVD + g * D + 8 * Lq, t, pos0) : zero;
             }
     };
-    load_v(0);
 
     // QK-norm + RoPE (qk_norm_rope_kernel arithmetic): wave 0 the query head, wave 1 the key
     // head, wave 2 copies the value row. Lane i holds elements i and i + 64, the pair RoPE
@@ -485,8 +516,8 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
             const float total = __uint_as_float(
                 __builtin_amdgcn_readfirstlane(__float_as_uint(group_sum<8>(acc))));
             const float inv = 1.0f / sqrtf(total / (float)D + a.eps);
-            const float ya = round_bf(round_bf(bf2f((bf16)xi) * inv) * pre.w0);
-            const float yb = round_bf(round_bf(bf2f((bf16)xj) * inv) * pre.w1);
+            const float ya = round_bf(round_bf(bf2f((bf16)xi) * inv) * bf2f((bf16)pre.w0));
+            const float yb = round_bf(round_bf(bf2f((bf16)xj) * inv) * bf2f((bf16)pre.w1));
             const float c = pre.cs[0], sn = pre.sn[0];
             const float a_cos = round_bf(ya * c), b_sin = round_bf(yb * sn);
             const float b_cos = round_bf(yb * c), a_sin = round_bf(ya * sn);
@@ -515,23 +546,24 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
     {
         const u32x4 qv = sm.q[Lp];
         const u32x4 kcur = sm.k[Lp];
+        // the 16 lanes of a position reduce the round's SCORE_LOADS dot products together
+        // (reduce-scatter, each total bit-identical to group_sum<16>): lane Lp < SCORE_LOADS
+        // ends with the key slot scatter_row(Lp)
+        const int us = scatter_row<SCORE_LOADS>(Lp);
         for (int base = 0; base < n; base += SCORE_LOADS * 4 * WAVES) {
-            u32x4 kv[SCORE_LOADS];
+            float part[SCORE_LOADS];
 #pragma unroll
             for (int u = 0; u < SCORE_LOADS; u++) {
                 const int t = key_slot(base, u);
-                if (base == 0) kv[u] = t == pos ? kcur : pre.k[u];
-                else kv[u] = t < pos ? ld_kv(kc + (size_t)t * KVD + g * D + 8 * Lp, t, pos0)
-                                     : (t == pos ? kcur : zero);
+                u32x4 kv;
+                if (base == 0) kv = t == pos ? kcur : pre.k[u];
+                else kv = t < pos ? ld_kv(kc + (size_t)t * KVD + g * D + 8 * Lp, t, pos0)
+                                  : (t == pos ? kcur : zero);
+                part[u] = dot8(qv, kv, 0.0f);
             }
-#pragma unroll
-            for (int u = 0; u < SCORE_LOADS; u++) {
-                if (base + u * 4 * WAVES >= n) break;  // the rest of the round is past pos
-                const int t = key_slot(base, u);
-                const float d = group_sum<16>(dot8(qv, kv[u], 0.0f));
-                const float s = round_bf(round_bf(d) * a.scale);
-                if (Lp == 0 && t < n) sm.sc[t] = s;
-            }
+            const float d = group_sum_scatter<16>(part);
+            const int t = key_slot(base, us);
+            if (Lp < SCORE_LOADS && t < n) sm.sc[t] = round_bf(round_bf(d) * a.scale);
         }
     }
     __syncthreads();
@@ -564,9 +596,11 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
         }
         __syncthreads();
         if (w < nb) {
-            const float M = wave_max(lane < nb ? sm.st[lane][0] : -__builtin_huge_valf());
-            const float sum =
-                wave_sum(lane < nb ? sm.st[lane][1] * exp_f32(sm.st[lane][0] - M) : 0.0f);
+            // lanes 0..7 hold the blocks (the rest would add -inf to the max and 0 to the sum,
+            // so the 8-lane trees give the 64-lane results)
+            const int b = lane & 7;
+            const float M = group_max<8>(b < nb ? sm.st[b][0] : -__builtin_huge_valf());
+            const float sum = group_sum<8>(b < nb ? sm.st[b][1] * exp_f32(sm.st[b][0] - M) : 0.0f);
             if (v) sm.sc[w * 64 + lane] = round_bf(exp_f32(s - M) / sum);
         }
         __syncthreads();
@@ -660,12 +694,14 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
 
 // Rows [r0, r1) of a phase with R rows owned by wave w of this workgroup, the rows spread in
 // order over waves FIRST_W..7 of workgroups first_wg.. (so a workgroup owns rows iff its wave
-// FIRST_W does). Waves below FIRST_W own none.
+// FIRST_W does, and few workgroups take part in a small phase: each one polls the phase's
+// input, and fewer pollers see a written vector sooner). Waves below FIRST_W own none; an
+// empty range is [R, R).
+__host__ __device__ constexpr int rows_per_wave(int R, int n_waves) { return (R + n_waves - 1) / n_waves; }
 template <int FIRST_W>
 __device__ __forceinline__ void phase_rows(int R, int first_wg, int w, int &r0, int &r1) {
     constexpr int RW = WAVES - FIRST_W;
-    const int nw = ((int)gridDim.x - first_wg) * RW;
-    const int per = (R + nw - 1) / nw;
+    const int per = rows_per_wave(R, ((int)gridDim.x - first_wg) * RW);
     const int gw = ((int)blockIdx.x - first_wg) * RW + w - FIRST_W;
     const bool none = (int)blockIdx.x < first_wg || w < FIRST_W;
     r0 = none ? R : min(R, gw * per);
@@ -681,6 +717,14 @@ __device__ __forceinline__ bool workgroup_has_rows(int R, int first_wg) {
     phase_rows<FIRST_W>(R, first_wg, FIRST_W, r0, r1);
     return r0 < r1;
 }
+
+// When a matrix workgroup requests the down rows and the next layer's q/k/v rows. Loads
+// complete in order, so a request placed before a poll holds the poll until it lands.
+enum {
+    PF_WITH_ATTENTION = 0,  // with the o and gate/up rows, while attention runs
+    PF_AFTER_POLL = 1,      // down rows once the o input is staged, q/k/v once gate/up's is
+    PF_AFTER_COMPUTE = 2,   // down rows after the gate/up rows, q/k/v after the down rows
+};
 
 template <class S>
 __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
@@ -754,6 +798,17 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
         };
     };
 
+    // Weight requests are unconditional: a wave without rows in a phase has the empty range
+    // [R, R) and loads row R - 1 (a cache hit after its owner's load). A request made on some
+    // paths only would leave the registers to be merged where the paths join, and the copy
+    // made there waits for the load (and, loads completing in order, for every earlier one).
+    // The first layer's q/k/v rows of the next token, requested before the token is known
+    // (by the last layer of the previous token after the first).
+    Rows<NCH, S::B_QKV> pf_qkv;
+    NormW<H> nq;  // attn_norm weights of the coming q/k/v phase
+    nq.load(klayer(kargs(), 0).attn_norm);
+    pf_qkv.load(qkv_row(klayer(kargs(), 0)), q0, q1);
+
     for (int step = 0; step < n_tokens; step++, pos++) {
     const unsigned sq0 = seq0 + step * seq_step;  // this token's first tag
     stamp<S>(0, step);
@@ -780,11 +835,8 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
             const uint16_t *erow = (const uint16_t *)(kargs().embed + (size_t)token * H);
             xown = o0 + lane < o1 ? (uint32_t)gptr(erow)[o0 + lane] : 0u;
         }
-        Rows<NCH, S::B_QKV> pf_qkv{};
-        NormW<H> nq{};  // attn_norm weights of the coming q/k/v phase
-        if (wg_q) nq.load(klayer(kargs(), 0).attn_norm);
-        if (q0 < q1) pf_qkv.load(qkv_row(klayer(kargs(), 0)), q0, q1);
         for (int l = 0; l < n_layers; l++) {
+            const int ln = l + 1 < n_layers ? l + 1 : 0;  // the layer whose q/k/v rows come next
             const unsigned seq = sq0 + PHASES * l;
             // ---- rmsnorm + q/k/v rows (weights requested a phase ahead)
             if (wg_q) {
@@ -818,19 +870,18 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
             Rows<NCH, S::B_GU> pf_g{}, pf_u{};
             Rows<NCI, S::B_DOWN> pf_d{};
             NormW<H> ng{};  // mlp_norm weights
-            if (o0 < o1) pf_o.load(o_row(klayer(kargs(), l)), o0, o1);
-            if (wg_g) ng.load(klayer(kargs(), l).mlp_norm);
-            if (g0 < g1) {
+            pf_o.load(o_row(klayer(kargs(), l)), o0, o1);
+            ng.load(klayer(kargs(), l).mlp_norm);
+            {
                 KLayer &L = klayer(kargs(), l);
                 const bf16 *wg = L.w_gate, *wu = L.w_up;
                 pf_g.load([=](int r) { return wg + (size_t)r * H; }, g0, g1);
                 pf_u.load([=](int r) { return wu + (size_t)r * H; }, g0, g1);
             }
-            if constexpr (S::PF_EARLY) {
-                if (o0 < o1) pf_d.load(d_row(klayer(kargs(), l)), o0, o1);
-                if (wg_q && l + 1 < n_layers) nq.load(klayer(kargs(), l + 1).attn_norm);
-                if (q0 < q1 && l + 1 < n_layers)
-                    pf_qkv.load(qkv_row(klayer(kargs(), l + 1)), q0, q1);
+            if constexpr (S::PF == PF_WITH_ATTENTION) {
+                pf_d.load(d_row(klayer(kargs(), l)), o0, o1);
+                nq.load(klayer(kargs(), ln).attn_norm);
+                pf_qkv.load(qkv_row(klayer(kargs(), ln)), q0, q1);
             }
             // ---- o rows + residual
             if (wg_o)
@@ -838,6 +889,9 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                                      kargs().error_flag);
             stamp<S>(2 + 4 * l, step);
             stamp_wg(l, n_layers, 2, step);
+            if constexpr (S::PF == PF_AFTER_POLL) {
+                pf_d.load(d_row(klayer(kargs(), l)), o0, o1);
+            }
             if (o0 < o1) {
                 u32x4 in[NCO];
                 lds_chunks<NCO>(sm.vec, in);
@@ -852,6 +906,11 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                                     kargs().error_flag);
             stamp<S>(3 + 4 * l, step);
             stamp_wg(l, n_layers, 4, step);
+            if constexpr (S::PF == PF_AFTER_POLL) {
+                // the next layer's q/k/v rows stream during gate/up, down and their handoffs
+                nq.load(klayer(kargs(), ln).attn_norm);
+                pf_qkv.load(qkv_row(klayer(kargs(), ln)), q0, q1);
+            }
             if (wg_g) wg_rmsnorm<H>(sm.vec, ng, kargs().eps, &norm_inv);
             if (g0 < g1) {
                 KArgs &a = kargs();
@@ -868,8 +927,8 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                 });
             }
             stamp_wg(l, n_layers, 5, step);
-            if constexpr (!S::PF_EARLY) {
-                if (o0 < o1) pf_d.load(d_row(klayer(kargs(), l)), o0, o1);
+            if constexpr (S::PF == PF_AFTER_COMPUTE) {
+                pf_d.load(d_row(klayer(kargs(), l)), o0, o1);
             }
             // ---- down rows + residual
             if (wg_o)
@@ -886,10 +945,9 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                                                              &xown);
             }
             stamp_wg(l, n_layers, 7, step);
-            if constexpr (!S::PF_EARLY) {
-                if (wg_q && l + 1 < n_layers) nq.load(klayer(kargs(), l + 1).attn_norm);
-                if (q0 < q1 && l + 1 < n_layers)
-                    pf_qkv.load(qkv_row(klayer(kargs(), l + 1)), q0, q1);
+            if constexpr (S::PF == PF_AFTER_COMPUTE) {
+                nq.load(klayer(kargs(), ln).attn_norm);
+                pf_qkv.load(qkv_row(klayer(kargs(), ln)), q0, q1);
             }
         }
     }
@@ -905,7 +963,7 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
         Rows<NCH, S::B_LM> batch{};
         NormW<H> nf{};  // final_norm weights
         nf.load(kargs().final_norm);
-        if (r0 < r1) batch.load(lm_row, r0, r1);
+        batch.load(lm_row, r0, r1);
         stage_vector<H, OW>(my_copy<H>(kargs().tx), tag_of(seq_end - 1), sm.vec,
                             kargs().error_flag);
         stamp<S>(1 + 4 * n_layers, step);
@@ -1014,8 +1072,9 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
 // ------------------------------------------------------------------------------------------
 
 // Compile-time shapes with the per-phase rows-per-batch choices (VGPR budget of 2 waves/SIMD)
-// for a grid of 256 workgroups: the matrix rows spread over (256 - HQ) * 8 waves. PF_EARLY:
-// the down rows and the next layer's q/k/v rows are also requested while attention runs.
+// for a grid of 256 workgroups: the matrix rows spread over (256 - HQ) * 8 waves. PF: when
+// the down rows and the next layer's q/k/v rows are requested (the o and gate/up rows always
+// go out while attention runs).
 template <int H_, int I_, int HQ_, int HKV_>
 struct Shape {
     static constexpr int H = H_, I = I_, HQ = HQ_, HKV = HKV_;
@@ -1025,7 +1084,7 @@ struct Shape {
     static constexpr int B_GU = H <= 1024 ? 2 : 1;
     static constexpr int B_DOWN = 1;
     static constexpr int B_LM = H <= 1024 ? 8 : (H <= 2048 ? 4 : 2);
-    static constexpr bool PF_EARLY = H <= 1024;
+    static constexpr int PF = H <= 1024 ? PF_WITH_ATTENTION : PF_AFTER_COMPUTE;
     // wave 0 of every workgroup stages the vectors and owns no matrix rows (so no weight load
     // is in flight in the polling wave); the larger shapes' vectors need every wave to poll
     static constexpr bool POLLER = false;
@@ -1053,8 +1112,8 @@ static const void *step_kernel_for(const Config *c) {
 // at most 64 residual rows per matrix wave (7 matrix waves per workgroup when wave 0 polls).
 static bool step_grid_fits(const Config *c, int grid) {
     if (grid <= 0 || grid > 1024 || grid < 2 * c->n_heads) return false;
-    const int waves = (grid - c->n_heads) * (WAVES - 1);
-    return (c->hidden_size + waves - 1) / waves <= 64;
+    // a wave keeps its residual rows of x in one register (lane j: its row j)
+    return rows_per_wave(c->hidden_size, (grid - c->n_heads) * WAVES) <= 64;
 }
 
 size_t step_workspace_bytes(const Config *c) {
