@@ -46,15 +46,23 @@ __device__ __forceinline__ float lo_f(uint32_t w) { return __uint_as_float(w << 
 __device__ __forceinline__ float hi_f(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
-// fp32 -> bf16 round to nearest even; NaN stays NaN with the quiet bit set.
+// fp32 -> bf16 round to nearest even; NaN stays NaN with the quiet bit set (the upper half of
+// the fp32 pattern | 0x40), denormals rounded like normals: the arithmetic of the integer form
+// (u + 0x7fff + ((u >> 16) & 1)) >> 16 for non-NaN u. gfx950 does it in one instruction
+// (v_cvt_pk_bf16_f32, two values at once), which gives the same bits for every input class.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t f2bf(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    const __bf16 b = (__bf16)f;
+    uint16_t u;
+    __builtin_memcpy(&u, &b, 2);
+    return u;
 }
 __device__ __forceinline__ float round_bf(float f) { return __uint_as_float(f2bf(f) << 16); }
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-    return f2bf(lo) | (f2bf(hi) << 16);
+    const bf16x2_t v = {(__bf16)lo, (__bf16)hi};
+    uint32_t u;
+    __builtin_memcpy(&u, &v, 4);
+    return u;
 }
 
 // Element e (0..7) of a chunk as fp32.
