@@ -35,6 +35,8 @@ namespace {
 constexpr int WAVES = 8;                   // waves per workgroup
 constexpr int THREADS = 64 * WAVES;
 constexpr long long SPIN_LIMIT = 1 << 22;  // polls before a wait gives up (~ seconds)
+// Pause between polls (s_sleep units of 64 clocks): polling traffic slows the memory side.
+constexpr int POLL_SLEEP = 1;
 constexpr int PHASES = 5;                  // tagged vectors written per layer
 
 // ---------------------------------------------------------------- coherent access
@@ -119,18 +121,17 @@ __device__ __forceinline__ void stage_pairs(Src src, uint32_t tag, uint32_t *dst
     __syncthreads();
     if (!ONE_WAVE || (tid_x() >> 6) == 0) {
         const int t0 = ONE_WAVE ? (tid_x() & 63) : (int)threadIdx.x;
+        // Every lane issues every poll (a lane past the pairs re-reads the last one), so no
+        // branch surrounds a load.
         uint64_t w[P];
         long long spins = 0;
         for (;;) {
             bool fresh = true;
 #pragma unroll
             for (int j = 0; j < P; j++) {
-                const int p = t0 + STEP * j;
-                if (p < PAIRS) {
-                    w[j] = ld_coh64(src(p));
-                    fresh &= (uint32_t)(w[j] & 0xffffu) == tag &&
-                             (uint32_t)((w[j] >> 32) & 0xffffu) == tag;
-                }
+                w[j] = ld_coh64(src(min(t0 + STEP * j, PAIRS - 1)));
+                fresh &= (uint32_t)(w[j] & 0xffffu) == tag &&
+                         (uint32_t)((w[j] >> 32) & 0xffffu) == tag;
             }
             if (fresh) break;
             if ((++spins & 63) == 0 &&
@@ -138,7 +139,7 @@ __device__ __forceinline__ void stage_pairs(Src src, uint32_t tag, uint32_t *dst
                 __hip_atomic_store(gptr(err), 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
             }
-            __builtin_amdgcn_s_sleep(1);
+            __builtin_amdgcn_s_sleep(POLL_SLEEP);
         }
 #pragma unroll
         for (int j = 0; j < P; j++) {
@@ -551,15 +552,22 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
         // ends with the key slot scatter_row(Lp)
         const int us = scatter_row<SCORE_LOADS>(Lp);
         for (int base = 0; base < n; base += SCORE_LOADS * 4 * WAVES) {
+            u32x4 kv[SCORE_LOADS];  // keys of a later round, all requested before the first use
+            if (base > 0) {
+#pragma unroll
+                for (int u = 0; u < SCORE_LOADS; u++) {
+                    const int t = key_slot(base, u);
+                    kv[u] = t < pos ? ld_kv(kc + (size_t)t * KVD + g * D + 8 * Lp, t, pos0)
+                                    : (t == pos ? kcur : zero);
+                }
+            }
             float part[SCORE_LOADS];
 #pragma unroll
             for (int u = 0; u < SCORE_LOADS; u++) {
+                part[u] = 0.0f;
+                if (base + u * 4 * WAVES >= n) continue;  // the slot's 32 positions are past pos
                 const int t = key_slot(base, u);
-                u32x4 kv;
-                if (base == 0) kv = t == pos ? kcur : pre.k[u];
-                else kv = t < pos ? ld_kv(kc + (size_t)t * KVD + g * D + 8 * Lp, t, pos0)
-                                  : (t == pos ? kcur : zero);
-                part[u] = dot8(qv, kv, 0.0f);
+                part[u] = dot8(qv, base == 0 ? (t == pos ? kcur : pre.k[u]) : kv[u], 0.0f);
             }
             const float d = group_sum_scatter<16>(part);
             const int t = key_slot(base, us);
@@ -664,11 +672,20 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
                     for (int e = 0; e < 8; e++) acc[e] = fmaf(p, elem(vt, e), acc[e]);
                 }
             }
+            // the four slot groups (lanes 16 apart) summed with the pairing of butterfly_sum<16,
+            // 64> (xor 16, then xor 32), reduce-scattered: the lane ends with elements d0, d0 + 1
+            float half[4], two[2];
+            const bool up16 = (G & 1) != 0, up32 = (G & 2) != 0;
 #pragma unroll
-            for (int e = 0; e < 8; e++) acc[e] = butterfly_sum<16, 64>(acc[e]);
-            if (G == 0)
+            for (int e = 0; e < 4; e++)
+                half[e] = (up16 ? acc[e + 4] : acc[e]) + xor_lane<16>(up16 ? acc[e] : acc[e + 4]);
 #pragma unroll
-                for (int e = 0; e < 8; e++) sm.quarter[(w >> 2) + 2 * j][qtr][8 * Lp + e] = acc[e];
+            for (int e = 0; e < 2; e++)
+                two[e] = (up32 ? half[e + 2] : half[e]) + xor_lane<32>(up32 ? half[e] : half[e + 2]);
+            const int d0 = (up16 ? 4 : 0) + (up32 ? 2 : 0);
+            float *qd = &sm.quarter[(w >> 2) + 2 * j][qtr][8 * Lp + d0];
+            qd[0] = two[0];
+            qd[1] = two[1];
         }
         __syncthreads();
         if (threadIdx.x < D) {
