@@ -467,8 +467,10 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
         const int qo = h * D, ko = QD + g * D, vo = QD + KVD + g * D;
         stage_pairs<3 * D / 2, false>(
             [=](int p) {
+                // segment p / 64: q, k or v (arithmetic, not a select chain, which the compiler
+                // turns into a table in scratch memory)
                 const int seg = p / (D / 2), i = 2 * (p % (D / 2));
-                return qkv + (seg == 0 ? qo : seg == 1 ? ko : vo) + i;
+                return qkv + qo + (seg >= 1) * (ko - qo) + (seg >= 2) * (vo - ko) + i;
             },
             tag_in, &sm.raw[0][0], a.error_flag);
     }
