@@ -122,7 +122,8 @@ typedef struct {
 } RunState;
 
 /* How capture_graph prepares the step. STEP_AUTO: the persistent step kernel (one cooperative
- * launch per token) when the shapes have a specialisation, else a hipGraph of the per-layer
+ * launch per forward; generate_greedy runs all its tokens in one launch) when the shapes have a
+ * specialisation, else a hipGraph of the per-layer
  * kernels. STEP_GRAPH: always the hipGraph. STEP_PERSISTENT: the persistent kernel or an
  * error. */
 enum { STEP_AUTO = 0, STEP_GRAPH = 1, STEP_PERSISTENT = 2 };
