@@ -752,8 +752,10 @@ __device__ __forceinline__ bool workgroup_has_rows(int R, int first_wg) {
     return r0 < r1;
 }
 
-// When a matrix workgroup requests the down rows and the next layer's q/k/v rows. Loads
-// complete in order, so a request placed before a poll holds the poll until it lands.
+// When a matrix workgroup requests the down rows (PF_D) and the next layer's q/k/v rows
+// (PF_QKV). Loads complete in order, so a request placed before a poll holds the poll until it
+// lands, and weights streaming during a handoff slow it: at 0.6B both go out while attention
+// runs (the q/k/v rows after the gate/up poll measured 7% slower, after the down rows 1.4%).
 enum {
     PF_WITH_ATTENTION = 0,  // with the o and gate/up rows, while attention runs
     PF_AFTER_POLL = 1,      // down rows once the o input is staged, q/k/v once gate/up's is
@@ -920,8 +922,8 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                 pf_g.load([=](int r) { return wg + (size_t)r * H; }, g0, g1);
                 pf_u.load([=](int r) { return wu + (size_t)r * H; }, g0, g1);
             }
-            if constexpr (S::PF == PF_WITH_ATTENTION) {
-                pf_d.load(d_row(klayer(kargs(), l)), o0, o1);
+            if constexpr (S::PF_D == PF_WITH_ATTENTION) pf_d.load(d_row(klayer(kargs(), l)), o0, o1);
+            if constexpr (S::PF_QKV == PF_WITH_ATTENTION) {
                 nq.load(klayer(kargs(), ln).attn_norm);
                 pf_qkv.load(qkv_row(klayer(kargs(), ln)), q0, q1);
             }
@@ -931,9 +933,7 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                                      kargs().error_flag);
             stamp<S>(2 + 4 * l, step);
             stamp_wg(l, n_layers, 2, step);
-            if constexpr (S::PF == PF_AFTER_POLL) {
-                pf_d.load(d_row(klayer(kargs(), l)), o0, o1);
-            }
+            if constexpr (S::PF_D == PF_AFTER_POLL) pf_d.load(d_row(klayer(kargs(), l)), o0, o1);
             if (wg_o) {
                 if (o0 < o1) {
                     u32x4 in[NCO];
@@ -952,7 +952,7 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                                     kargs().error_flag);
             stamp<S>(3 + 4 * l, step);
             stamp_wg(l, n_layers, 4, step);
-            if constexpr (S::PF == PF_AFTER_POLL) {
+            if constexpr (S::PF_QKV == PF_AFTER_POLL) {
                 // the next layer's q/k/v rows stream during gate/up, down and their handoffs
                 nq.load(klayer(kargs(), ln).attn_norm);
                 pf_qkv.load(qkv_row(klayer(kargs(), ln)), q0, q1);
@@ -973,9 +973,7 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                 });
             }
             stamp_wg(l, n_layers, 5, step);
-            if constexpr (S::PF == PF_AFTER_COMPUTE) {
-                pf_d.load(d_row(klayer(kargs(), l)), o0, o1);
-            }
+            if constexpr (S::PF_D == PF_AFTER_COMPUTE) pf_d.load(d_row(klayer(kargs(), l)), o0, o1);
             // ---- down rows + residual
             if (wg_o)
                 stage_vector<I, OW>(my_copy<I>(kargs().thb), tag_of(seq + 3), sm.vec,
@@ -994,7 +992,7 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                 if ((tid_x() >> 6) == FW) publish_rows<H>(kargs().tx, out_stage, wr0, wr1);
             }
             stamp_wg(l, n_layers, 7, step);
-            if constexpr (S::PF == PF_AFTER_COMPUTE) {
+            if constexpr (S::PF_QKV == PF_AFTER_COMPUTE) {
                 nq.load(klayer(kargs(), ln).attn_norm);
                 pf_qkv.load(qkv_row(klayer(kargs(), ln)), q0, q1);
             }
@@ -1133,7 +1131,8 @@ struct Shape {
     static constexpr int B_GU = H <= 1024 ? 2 : 1;
     static constexpr int B_DOWN = 1;
     static constexpr int B_LM = H <= 1024 ? 8 : (H <= 2048 ? 4 : 2);
-    static constexpr int PF = H <= 1024 ? PF_WITH_ATTENTION : PF_AFTER_COMPUTE;
+    static constexpr int PF_D = H <= 1024 ? PF_WITH_ATTENTION : PF_AFTER_COMPUTE;
+    static constexpr int PF_QKV = H <= 1024 ? PF_WITH_ATTENTION : PF_AFTER_COMPUTE;
     // wave 0 of every workgroup stages the vectors and owns no matrix rows (so no weight load
     // is in flight in the polling wave); the larger shapes' vectors need every wave to poll
     static constexpr bool POLLER = false;

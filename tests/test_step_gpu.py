@@ -314,6 +314,38 @@ def test_persistent_generate_one_launch_small(gpu, oracle):
         dec.close()
 
 
+@pytest.mark.parametrize("size", ["1.7B", "4B"])
+def test_persistent_step_wide_shapes(gpu, oracle, size):
+    """The Qwen3-1.7B and -4B specialisations of the persistent step (their widths and heads,
+    3 layers to keep the oracle quick): logits and argmax bit-identical to the oracle at 70
+    positions (two 64-position attention blocks), then a one-launch generate of 20 tokens equal
+    to the oracle's greedy tokens."""
+    ident(f"persistent step {size} widths")
+    from llm_inference_amd import model
+    cfg = model.qwen3_config(size, n_layers=3, max_seq_len=128)
+    dec = model.Decoder(cfg, ("synth", 11, 0.02, 0.1))
+    try:
+        dec.capture_graph("persistent")
+        assert dec.persistent
+        w = dec.host_weights()
+        orc = oracle.Model(oracle_cfg(cfg), w, max_seq=128)
+        tokens = [int(t) for t in np.random.default_rng(12).integers(0, cfg.vocab_size, 70)]
+        for pos, tok in enumerate(tokens):
+            dec.forward(tok, pos)
+            nxt = dec.sample_argmax()
+            ref = orc.forward(tok, pos, oracle.GPU_ORDER)
+            assert np.array_equal(dec.logits(), orc.logits), pos
+            assert nxt == ref, pos
+        got = dec.generate_greedy(nxt, len(tokens), 20)
+        t, want = nxt, []
+        for i in range(20):
+            t = orc.forward(t, len(tokens) + i, oracle.GPU_ORDER)
+            want.append(t)
+        assert got == want
+    finally:
+        dec.close()
+
+
 def test_persistent_step_long_context(qwen06b, oracle):
     """One decode position at 5000 with the KV cache below it filled with N(0, 1): the
     persistent step's attention over 79 blocks of 64 positions is bit-identical to the
