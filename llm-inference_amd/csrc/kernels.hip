@@ -236,7 +236,8 @@ enum { EPI_PLAIN = 0, EPI_RESID = 1 };
 template <int NC, int RPW, int EPI>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     const int lane = threadIdx.x & 63;
-    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    // wave-uniform (scalar), so the per-row buffer descriptors below are scalar too
+    const int wave = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int si = (a.n_seg > 2 && wave >= a.seg[2].wave_begin)   ? 2
                    : (a.n_seg > 1 && wave >= a.seg[1].wave_begin) ? 1
                                                                   : 0;
@@ -248,26 +249,28 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     if (row0 >= rows) return;
     const int cols = a.cols;
     const int n_chunks = cols >> 3;
+    const __amdgpu_buffer_rsrc_t xr =
+        __builtin_amdgcn_make_buffer_rsrc((void *)a.x, (short)0, cols * 2, BUFFER_FLAGS);
     float acc[RPW];
 #pragma unroll
     for (int i = 0; i < RPW; i++) acc[i] = 0.0f;
     for (int c0 = 0; c0 < n_chunks; c0 += 64 * NC) {
-        u32x4 xv[NC];
         u32x4 wv[RPW][NC];
+        u32x4 xv[NC];
 #pragma unroll
-        for (int k = 0; k < NC; k++) {
-            const int c = c0 + lane + 64 * k;
-            xv[k] = c < n_chunks ? ld16(a.x + 8 * (size_t)c) : u32x4{0, 0, 0, 0};
-        }
+        for (int k = 0; k < NC; k++)
+            xv[k] = __builtin_amdgcn_raw_buffer_load_b128(xr, 16 * (c0 + lane + 64 * k), 0, 0);
 #pragma unroll
         for (int i = 0; i < RPW; i++) {
+            // the row as a buffer: chunks past its end read as zeros with no branch around the
+            // loads, so each chunk's FMAs wait only for that chunk's load
             const int r = min(row0 + i, rows - 1);
-            const bf16 *wr = w + (size_t)r * cols;
+            const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+                (void *)(w + (size_t)r * cols), (short)0, cols * 2, BUFFER_FLAGS);
 #pragma unroll
-            for (int k = 0; k < NC; k++) {
-                const int c = c0 + lane + 64 * k;
-                wv[i][k] = c < n_chunks ? ld16_nt(wr + 8 * (size_t)c) : u32x4{0, 0, 0, 0};
-            }
+            for (int k = 0; k < NC; k++)
+                wv[i][k] = __builtin_amdgcn_raw_buffer_load_b128(rs, 16 * (c0 + lane + 64 * k), 0,
+                                                                 BUFFER_NT);
         }
 #pragma unroll
         for (int i = 0; i < RPW; i++)
@@ -299,10 +302,12 @@ __global__ __launch_bounds__(256) void gate_up_kernel(bf16 *act, const bf16 *wg,
                                                       const bf16 *x, int rows, int cols,
                                                       bf16 *gate_tap, bf16 *up_tap) {
     const int lane = threadIdx.x & 63;
-    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int wave = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int row0 = wave * RPW;
     if (row0 >= rows) return;
     const int n_chunks = cols >> 3;
+    const __amdgpu_buffer_rsrc_t xr =
+        __builtin_amdgcn_make_buffer_rsrc((void *)x, (short)0, cols * 2, BUFFER_FLAGS);
     float ag[RPW], au[RPW];
 #pragma unroll
     for (int i = 0; i < RPW; i++) ag[i] = au[i] = 0.0f;
@@ -310,19 +315,20 @@ __global__ __launch_bounds__(256) void gate_up_kernel(bf16 *act, const bf16 *wg,
         u32x4 xv[NC];
         u32x4 gv[RPW][NC], uv[RPW][NC];
 #pragma unroll
-        for (int k = 0; k < NC; k++) {
-            const int c = c0 + lane + 64 * k;
-            xv[k] = c < n_chunks ? ld16(x + 8 * (size_t)c) : u32x4{0, 0, 0, 0};
-        }
+        for (int k = 0; k < NC; k++)
+            xv[k] = __builtin_amdgcn_raw_buffer_load_b128(xr, 16 * (c0 + lane + 64 * k), 0, 0);
 #pragma unroll
         for (int i = 0; i < RPW; i++) {
             const size_t r = (size_t)min(row0 + i, rows - 1);
+            const __amdgpu_buffer_rsrc_t rg = __builtin_amdgcn_make_buffer_rsrc(
+                (void *)(wg + r * cols), (short)0, cols * 2, BUFFER_FLAGS);
+            const __amdgpu_buffer_rsrc_t ru = __builtin_amdgcn_make_buffer_rsrc(
+                (void *)(wu + r * cols), (short)0, cols * 2, BUFFER_FLAGS);
 #pragma unroll
             for (int k = 0; k < NC; k++) {
-                const int c = c0 + lane + 64 * k;
-                const bool in = c < n_chunks;
-                gv[i][k] = in ? ld16_nt(wg + r * cols + 8 * (size_t)c) : u32x4{0, 0, 0, 0};
-                uv[i][k] = in ? ld16_nt(wu + r * cols + 8 * (size_t)c) : u32x4{0, 0, 0, 0};
+                const int off = 16 * (c0 + lane + 64 * k);
+                gv[i][k] = __builtin_amdgcn_raw_buffer_load_b128(rg, off, 0, BUFFER_NT);
+                uv[i][k] = __builtin_amdgcn_raw_buffer_load_b128(ru, off, 0, BUFFER_NT);
             }
         }
 #pragma unroll
