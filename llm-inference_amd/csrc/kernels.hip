@@ -890,16 +890,25 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnArgs a) {
     }
 }
 
-// Pass 3: out = bf16(block partials added in block order).
+// Pass 3: out = bf16(block partials added in block order). The additions are sequential, the
+// loads are not: 16 partials per thread are requested before any is added.
 template <int D>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
+    constexpr int BATCH = 16;
     const int h = blockIdx.x;
     const int n = *a.d_pos + 1;
     const int nb = (n + ATT_B - 1) / ATT_B;
     for (int d = threadIdx.x; d < D; d += blockDim.x) {
         const float *p = a.partial + (size_t)h * a.max_blocks * D + d;
         float acc = p[0];
-        for (int b = 1; b < nb; b++) acc = acc + p[(size_t)b * D];
+        for (int b0 = 1; b0 < nb; b0 += BATCH) {
+            float v[BATCH];
+#pragma unroll
+            for (int j = 0; j < BATCH; j++) v[j] = p[(size_t)min(b0 + j, nb - 1) * D];
+#pragma unroll
+            for (int j = 0; j < BATCH; j++)
+                if (b0 + j < nb) acc = acc + v[j];
+        }
         a.out[(size_t)h * D + d] = (bf16)f2bf(acc);
     }
 }
