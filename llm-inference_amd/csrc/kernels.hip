@@ -737,6 +737,25 @@ extern "C" void qk_norm_rope_rows(bf16 *q, bf16 *k, const bf16 *v, const bf16 *q
 
 constexpr int ATT_B = 64;  // positions per block
 
+// Reduce-scatter of M values per lane over aligned lane groups of N, from xor distance S on:
+// at each step a lane keeps half of its values (the upper half when bit S of its lane index is
+// set) and adds its partner's copies of them, so every total has the pairing of the butterfly
+// sum; `out` receives the M * S / N values left.
+template <int M, int S, int N>
+__device__ __forceinline__ void scatter_keep(const float *v, float *out) {
+    if constexpr (S >= N) {
+#pragma unroll
+        for (int j = 0; j < M; j++) out[j] = v[j];
+    } else {
+        const bool up = (tid_x() & S) != 0;
+        float keep[M / 2];
+#pragma unroll
+        for (int j = 0; j < M / 2; j++)
+            keep[j] = (up ? v[j + M / 2] : v[j]) + xor_lane<S>(up ? v[j] : v[j + M / 2]);
+        scatter_keep<M / 2, 2 * S, N>(keep, out);
+    }
+}
+
 struct AttnArgs {
     bf16 *out;
     const bf16 *q;
@@ -781,18 +800,28 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(AttnArgs a) {
             const int t = b * ATT_B + w * PER_WAVE + it * PPW + G;
             kv[it] = t < n ? ld16_nt(a.kc + (size_t)t * kv_dim + g * D + 8 * L) : u32x4{0, 0, 0, 0};
         }
+        // the ITERS * REP dot products of a lane, reduced over the LP lanes of its position group
+        // LP at a time by reduce-scatter (each total bit-identical to group_sum<LP>): lane L of a
+        // slice ends with product scatter_row(L) of that slice
+        constexpr int NP = ITERS * REP, SL = NP < LP ? NP : LP;
+        float part[NP];
 #pragma unroll
-        for (int it = 0; it < ITERS; it++) {
+        for (int it = 0; it < ITERS; it++)
+#pragma unroll
+            for (int r = 0; r < REP; r++) part[it * REP + r] = dot8(qv[r], kv[it], 0.0f);
+#pragma unroll
+        for (int s0 = 0; s0 < NP; s0 += SL) {
+            float slice[SL];
+#pragma unroll
+            for (int j = 0; j < SL; j++) slice[j] = part[s0 + j];
+            const float d = group_sum_scatter<LP, SL>(slice);
+            const int j = s0 + scatter_row<SL>(L), it = j / REP, r = j - it * REP;
             const int slot = w * PER_WAVE + it * PPW + G;
             const int t = b * ATT_B + slot;
-#pragma unroll
-            for (int r = 0; r < REP; r++) {
-                const float d = group_sum<LP>(dot8(qv[r], kv[it], 0.0f));
-                const float s = round_bf(round_bf(d) * a.scale);
-                if (L == 0) {
-                    sc[r][slot] = s;
-                    if (t < n) a.scores[(size_t)(g * REP + r) * a.max_seq + t] = s;
-                }
+            const float s = round_bf(round_bf(d) * a.scale);
+            if (L < SL) {
+                sc[r][slot] = s;
+                if (t < n) a.scores[(size_t)(g * REP + r) * a.max_seq + t] = s;
             }
         }
         __syncthreads();
@@ -837,21 +866,44 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnArgs a) {
         for (int r = w; r < REP; r += 4) {
             const int h = g * REP + r;
             const float *st = a.stats + (size_t)h * a.max_blocks * 2;
-            float M = -__builtin_huge_valf();
-            for (int c0 = 0; c0 < nb; c0 += 64) {
-                const int bi = c0 + lane;
-                M = fmaxf(M, wave_max(bi < nb ? st[2 * bi] : -__builtin_huge_valf()));
-            }
-            float sum = 0.0f;
-            for (int c0 = 0; c0 < nb; c0 += 64) {
-                const int bi = c0 + lane;
-                const float term = bi < nb ? st[2 * bi + 1] * exp_f32(st[2 * bi] - M) : 0.0f;
-                const float cs = wave_sum(term);
-                sum = c0 == 0 ? cs : sum + cs;
-            }
             const int t = b * ATT_B + lane;
-            p_s[r][lane] =
-                t < n ? round_bf(exp_f32(a.scores[(size_t)h * a.max_seq + t] - M) / sum) : 0.0f;
+            const float s_t = a.scores[(size_t)h * a.max_seq + min(t, n - 1)];
+            float M = -__builtin_huge_valf(), sum = 0.0f;
+            constexpr int MAXC = 4;  // chunks of 64 block statistics held in registers
+            if (nb <= 64 * MAXC) {
+                // every statistic requested at once (clamped indices, no branch around the
+                // loads), then the same max and in-order chunk sums as below
+                float mv[MAXC], sv[MAXC];
+#pragma unroll
+                for (int c = 0; c < MAXC; c++) {
+                    const int bi = min(c * 64 + lane, nb - 1);
+                    mv[c] = st[2 * bi];
+                    sv[c] = st[2 * bi + 1];
+                }
+#pragma unroll
+                for (int c = 0; c < MAXC; c++)
+                    if (c * 64 < nb)
+                        M = fmaxf(M, wave_max(c * 64 + lane < nb ? mv[c] : -__builtin_huge_valf()));
+#pragma unroll
+                for (int c = 0; c < MAXC; c++)
+                    if (c * 64 < nb) {
+                        const float term = c * 64 + lane < nb ? sv[c] * exp_f32(mv[c] - M) : 0.0f;
+                        const float cs = wave_sum(term);
+                        sum = c == 0 ? cs : sum + cs;
+                    }
+            } else {
+                for (int c0 = 0; c0 < nb; c0 += 64) {
+                    const int bi = c0 + lane;
+                    M = fmaxf(M, wave_max(bi < nb ? st[2 * bi] : -__builtin_huge_valf()));
+                }
+                for (int c0 = 0; c0 < nb; c0 += 64) {
+                    const int bi = c0 + lane;
+                    const float term = bi < nb ? st[2 * bi + 1] * exp_f32(st[2 * bi] - M) : 0.0f;
+                    const float cs = wave_sum(term);
+                    sum = c0 == 0 ? cs : sum + cs;
+                }
+            }
+            p_s[r][lane] = t < n ? round_bf(exp_f32(s_t - M) / sum) : 0.0f;
         }
         __syncthreads();
         float acc[REP][8];
@@ -871,15 +923,24 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnArgs a) {
                 }
             }
         }
+        // the position groups (lanes LP apart) summed with the pairing of butterfly_sum<LP, 64>,
+        // reduce-scattered: each lane keeps REP * 8 / (64 / LP) of the values, at offset `off`
+        constexpr int NV = REP * 8, NG = 64 / LP, KEEP = NV / NG;
+        float flat[NV], kept[KEEP];
 #pragma unroll
         for (int r = 0; r < REP; r++)
 #pragma unroll
-            for (int e = 0; e < 8; e++) acc[r][e] = butterfly_sum<LP, 64>(acc[r][e]);
-        if (G == 0)
+            for (int e = 0; e < 8; e++) flat[r * 8 + e] = acc[r][e];
+        scatter_keep<NV, LP, 64>(flat, kept);
+        int off = 0;
 #pragma unroll
-            for (int r = 0; r < REP; r++)
+        for (int k = 0, m = NV; (LP << k) < 64; k++, m >>= 1)
+            if ((lane >> k) & LP) off += m / 2;
 #pragma unroll
-                for (int e = 0; e < 8; e++) red[w][r][8 * L + e] = acc[r][e];
+        for (int j = 0; j < KEEP; j++) {
+            const int idx = off + j, r = idx / 8, e = idx % 8;
+            red[w][r][8 * L + e] = kept[j];
+        }
         __syncthreads();
         for (int i = threadIdx.x; i < REP * D; i += 256) {
             const int r = i / D, d = i - r * D;
