@@ -89,6 +89,22 @@ void qk_norm_rope_rows(bf16 *q, bf16 *k, const bf16 *v, const bf16 *q_norm_w,
  * gate_up_forward (src/kernels.cu:283-286). */
 void swiglu_forward(bf16 *act, const bf16 *gate, const bf16 *up, size_t n, hipStream_t stream);
 
+/* RMSNorm of the single row x (as rmsnorm_forward, eps, weight norm_w) fused into the prologue
+ * of the GEMV that reads it: bit-identical to rmsnorm_forward into a temporary followed by
+ * qkv_forward / gemv_forward / gate_up_forward on it, without the temporary's store and reload
+ * or the extra launch. No counterpart in the reference: each replaces one rmsnorm_forward
+ * (src/kernels.cu:25-71) plus the launcher that consumes its output (qkv: src/kernels.cu:215-257,
+ * gemv: :79-212, gate_up: :260-298) in a decode step. cols % 8 == 0 and cols <= 8192 (the
+ * normed row stays in registers). */
+void rmsnorm_qkv_forward(bf16 *q, bf16 *k, bf16 *v, const bf16 *wq, const bf16 *wk,
+                         const bf16 *wv, const bf16 *x, const bf16 *norm_w, float eps, int q_rows,
+                         int kv_rows, int cols, hipStream_t stream);
+void rmsnorm_gemv_forward(bf16 *out, const bf16 *w, const bf16 *x, const bf16 *norm_w, float eps,
+                          int rows, int cols, hipStream_t stream);
+void rmsnorm_gate_up_forward(bf16 *act, const bf16 *w_gate, const bf16 *w_up, const bf16 *x,
+                             const bf16 *norm_w, float eps, int rows, int cols,
+                             hipStream_t stream);
+
 /* Floats attention_forward needs in `att` for these sizes. */
 size_t attention_workspace_floats(int n_heads, int head_dim, int max_seq);
 

@@ -20,7 +20,8 @@ __all__ = [
     "LlmError", "lib", "embedding_forward", "rmsnorm_forward", "gemv_forward",
     "gemv_residual_forward", "qkv_forward", "gate_up_forward", "qk_norm_rope_forward",
     "qk_norm_rope_rows", "attention_forward", "argmax_forward", "swiglu_forward",
-    "attention_workspace_floats", "EXPORTED_SYMBOLS",
+    "attention_workspace_floats", "rmsnorm_qkv_forward", "rmsnorm_gemv_forward",
+    "rmsnorm_gate_up_forward", "EXPORTED_SYMBOLS",
 ]
 
 # Every symbol include/llm_amd/*.h declares.
@@ -28,6 +29,7 @@ EXPORTED_SYMBOLS = [
     "embedding_forward", "rmsnorm_forward", "gemv_forward", "gemv_residual_forward",
     "qkv_forward", "gate_up_forward", "qk_norm_rope_forward", "attention_forward",
     "argmax_forward", "qk_norm_rope_rows", "swiglu_forward", "attention_workspace_floats",
+    "rmsnorm_qkv_forward", "rmsnorm_gemv_forward", "rmsnorm_gate_up_forward",
     "llm_set_exit_on_error", "llm_last_error", "llm_clear_error",
     "load_config", "load_weights", "free_weights", "print_weight_checksums",
     "alloc_run_state", "free_run_state", "capture_graph", "forward", "sample_argmax",
@@ -60,6 +62,9 @@ _SIGS = {
     "argmax_forward": (None, [_vp, _vp, _i, _vp]),
     "swiglu_forward": (None, [_vp, _vp, _vp, _sz, _vp]),
     "attention_workspace_floats": (_sz, [_i, _i, _i]),
+    "rmsnorm_qkv_forward": (None, [_vp] * 8 + [_f, _i, _i, _i, _vp]),
+    "rmsnorm_gemv_forward": (None, [_vp] * 4 + [_f, _i, _i, _vp]),
+    "rmsnorm_gate_up_forward": (None, [_vp] * 5 + [_f, _i, _i, _vp]),
     "llm_set_exit_on_error": (_i, [_i]),
     "llm_last_error": (ctypes.c_char_p, []),
     "llm_clear_error": (None, []),
@@ -162,6 +167,24 @@ def qkv_forward(q, k, v, wq, wk, wv, x, q_rows, kv_rows, cols, stream=None):
 def gate_up_forward(act, w_gate, w_up, x, rows, cols, gate_tap=None, up_tap=None, stream=None):
     _call(lib().gate_up_forward, _bf16(act, "act"), _bf16(w_gate, "w_gate"), _bf16(w_up, "w_up"),
           _bf16(x, "x"), rows, cols, _bf16(gate_tap, "gate_tap"), _bf16(up_tap, "up_tap"),
+          _stream(stream))
+
+
+def rmsnorm_qkv_forward(q, k, v, wq, wk, wv, x, norm_w, eps, q_rows, kv_rows, cols,
+                        stream=None):
+    _call(lib().rmsnorm_qkv_forward, _bf16(q, "q"), _bf16(k, "k"), _bf16(v, "v"),
+          _bf16(wq, "wq"), _bf16(wk, "wk"), _bf16(wv, "wv"), _bf16(x, "x"),
+          _bf16(norm_w, "norm_w"), eps, q_rows, kv_rows, cols, _stream(stream))
+
+
+def rmsnorm_gemv_forward(out, w, x, norm_w, eps, rows, cols, stream=None):
+    _call(lib().rmsnorm_gemv_forward, _bf16(out, "out"), _bf16(w, "w"), _bf16(x, "x"),
+          _bf16(norm_w, "norm_w"), eps, rows, cols, _stream(stream))
+
+
+def rmsnorm_gate_up_forward(act, w_gate, w_up, x, norm_w, eps, rows, cols, stream=None):
+    _call(lib().rmsnorm_gate_up_forward, _bf16(act, "act"), _bf16(w_gate, "w_gate"),
+          _bf16(w_up, "w_up"), _bf16(x, "x"), _bf16(norm_w, "norm_w"), eps, rows, cols,
           _stream(stream))
 
 

@@ -98,25 +98,43 @@ static bool forward_kernels(const Config *cfg, const Weights *w, RunState *s) {
     const int I = cfg->intermediate_size;
     const float scale = (float)(1.0 / sqrt((double)D));
     hipStream_t st = s->stream;
+    // RMSNorm runs as the prologue of the GEMV that reads it (same bits, one launch and one
+    // store/reload of the normed row fewer) for hidden sizes of up to 8192
+    const bool fuse_norm = H <= 8192;
     embedding_checked(s->x, w->embed, s->next_token, H, cfg->vocab_size, s->error_flag, st);
     for (int l = 0; l < cfg->n_layers && !llm_has_error(); l++) {
         const LayerWeights *L = &w->layers[l];
         bf16 *kc = s->key_cache + (size_t)l * s->max_seq * kv_dim;
         bf16 *vc = s->value_cache + (size_t)l * s->max_seq * kv_dim;
-        rmsnorm_forward(s->xb, s->x, L->attn_norm, 1, H, cfg->rms_norm_eps, st);
-        qkv_forward(s->q, s->k, s->v, L->wq, L->wk, L->wv, s->xb, q_dim, kv_dim, H, st);
+        if (fuse_norm) {
+            rmsnorm_qkv_forward(s->q, s->k, s->v, L->wq, L->wk, L->wv, s->x, L->attn_norm,
+                                cfg->rms_norm_eps, q_dim, kv_dim, H, st);
+        } else {
+            rmsnorm_forward(s->xb, s->x, L->attn_norm, 1, H, cfg->rms_norm_eps, st);
+            qkv_forward(s->q, s->k, s->v, L->wq, L->wk, L->wv, s->xb, q_dim, kv_dim, H, st);
+        }
         qk_norm_rope_forward(s->q, s->k, s->v, L->q_norm, L->k_norm, kc, vc, s->pos, cfg->n_heads,
                              cfg->n_kv_heads, D, cfg->rms_norm_eps, cfg->rope_theta, nullptr,
                              nullptr, st);
         attention_forward(s->attn_out, s->q, kc, vc, s->att, cfg->n_heads, cfg->n_kv_heads, D,
                           s->pos, s->max_seq, scale, st);
         gemv_residual_forward(s->x, L->wo, s->attn_out, H, q_dim, nullptr, st);
-        rmsnorm_forward(s->xb, s->x, L->mlp_norm, 1, H, cfg->rms_norm_eps, st);
-        gate_up_forward(s->hb, L->w_gate, L->w_up, s->xb, I, H, nullptr, nullptr, st);
+        if (fuse_norm) {
+            rmsnorm_gate_up_forward(s->hb, L->w_gate, L->w_up, s->x, L->mlp_norm,
+                                    cfg->rms_norm_eps, I, H, st);
+        } else {
+            rmsnorm_forward(s->xb, s->x, L->mlp_norm, 1, H, cfg->rms_norm_eps, st);
+            gate_up_forward(s->hb, L->w_gate, L->w_up, s->xb, I, H, nullptr, nullptr, st);
+        }
         gemv_residual_forward(s->x, L->w_down, s->hb, H, I, nullptr, st);
     }
-    rmsnorm_forward(s->xb, s->x, w->final_norm, 1, H, cfg->rms_norm_eps, st);
-    gemv_forward(s->logits, w->lm_head, s->xb, cfg->vocab_size, H, st);
+    if (fuse_norm) {
+        rmsnorm_gemv_forward(s->logits, w->lm_head, s->x, w->final_norm, cfg->rms_norm_eps,
+                             cfg->vocab_size, H, st);
+    } else {
+        rmsnorm_forward(s->xb, s->x, w->final_norm, 1, H, cfg->rms_norm_eps, st);
+        gemv_forward(s->logits, w->lm_head, s->xb, cfg->vocab_size, H, st);
+    }
     return !llm_has_error();
 }
 

@@ -225,15 +225,42 @@ struct GemvArgs {
     int n_seg;
     const bf16 *x;
     int cols;
-    bf16 *tap;  // residual epilogue: optional copy of y
+    bf16 *tap;             // residual epilogue: optional copy of y
+    const bf16 *norm_w;    // fused RMSNorm prologue: gamma (NORM kernels only)
+    float eps;
 };
+
+// The fused RMSNorm prologue of a one-panel GEMV: the wave's input chunks (lane l: chunks
+// l + 64k, the layout of rmsnorm_wave_kernel<NC>) normalised in registers with that kernel's
+// arithmetic, so the GEMV sees exactly the bf16 vector rmsnorm_forward would have written.
+template <int NC>
+__device__ __forceinline__ void norm_chunks(u32x4 (&xv)[NC], const bf16 *gamma, int cols, float eps) {
+    const int lane = tid_x() & 63;
+    const __amdgpu_buffer_rsrc_t gr =
+        __builtin_amdgcn_make_buffer_rsrc((void *)gamma, (short)0, cols * 2, BUFFER_FLAGS);
+    u32x4 gv[NC];
+#pragma unroll
+    for (int k = 0; k < NC; k++) gv[k] = __builtin_amdgcn_raw_buffer_load_b128(gr, 16 * (lane + 64 * k), 0, 0);
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < NC; k++) acc = dot8(xv[k], xv[k], acc);
+    const float total = wave_sum(acc);
+    const float inv = 1.0f / sqrtf(total / (float)cols + eps);
+#pragma unroll
+    for (int k = 0; k < NC; k++) {
+        float r[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) r[e] = round_bf(elem(xv[k], e) * inv) * elem(gv[k], e);
+        xv[k] = u32x4{pack2(r[0], r[1]), pack2(r[2], r[3]), pack2(r[4], r[5]), pack2(r[6], r[7])};
+    }
+}
 
 enum { EPI_PLAIN = 0, EPI_RESID = 1 };
 
 // Wave `wave` computes RPW consecutive rows. Lane l streams chunks l, l+64, ... of each row
 // (NC per lane per panel, panels until the row ends), fma-accumulating in order; the wave tree
 // then gives every lane each row's sum and lane i stores row row0+i.
-template <int NC, int RPW, int EPI>
+template <int NC, int RPW, int EPI, bool NORM = false>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     const int lane = threadIdx.x & 63;
     // wave-uniform (scalar), so the per-row buffer descriptors below are scalar too
@@ -260,6 +287,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 #pragma unroll
         for (int k = 0; k < NC; k++)
             xv[k] = __builtin_amdgcn_raw_buffer_load_b128(xr, 16 * (c0 + lane + 64 * k), 0, 0);
+        if constexpr (NORM) norm_chunks<NC>(xv, a.norm_w, cols, a.eps);  // one panel (host check)
 #pragma unroll
         for (int i = 0; i < RPW; i++) {
             // the row as a buffer: chunks past its end read as zeros with no branch around the
@@ -297,10 +325,12 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
 
 // gate and up rows together: g = bf16(wg[r].x), u = bf16(wu[r].x),
 // act = bf16(bf16(silu(g)) * u) (src/kernels.cu:276-287).
-template <int NC, int RPW>
+template <int NC, int RPW, bool NORM = false>
 __global__ __launch_bounds__(256) void gate_up_kernel(bf16 *act, const bf16 *wg, const bf16 *wu,
                                                       const bf16 *x, int rows, int cols,
-                                                      bf16 *gate_tap, bf16 *up_tap) {
+                                                      bf16 *gate_tap, bf16 *up_tap,
+                                                      const bf16 *norm_w = nullptr,
+                                                      float eps = 0.0f) {
     const int lane = threadIdx.x & 63;
     const int wave = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int row0 = wave * RPW;
@@ -317,6 +347,7 @@ __global__ __launch_bounds__(256) void gate_up_kernel(bf16 *act, const bf16 *wg,
 #pragma unroll
         for (int k = 0; k < NC; k++)
             xv[k] = __builtin_amdgcn_raw_buffer_load_b128(xr, 16 * (c0 + lane + 64 * k), 0, 0);
+        if constexpr (NORM) norm_chunks<NC>(xv, norm_w, cols, eps);  // one panel (host check)
 #pragma unroll
         for (int i = 0; i < RPW; i++) {
             const size_t r = (size_t)min(row0 + i, rows - 1);
@@ -395,7 +426,10 @@ template <int EPI>
 static bool dispatch_gemv(const GemvArgs &a, int nc, int rpw, int blocks, hipStream_t st) {
 #define X(NC_, RPW_)                                                         \
     if (nc == NC_ && rpw == RPW_) {                                          \
-        gemv_kernel<NC_, RPW_, EPI><<<blocks, 256, 0, st>>>(a);              \
+        if (EPI == EPI_PLAIN && a.norm_w)                                    \
+            gemv_kernel<NC_, RPW_, EPI_PLAIN, true><<<blocks, 256, 0, st>>>(a); \
+        else                                                                 \
+            gemv_kernel<NC_, RPW_, EPI><<<blocks, 256, 0, st>>>(a);          \
         return LAUNCH_OK();                                                  \
     }
     GEMV_CASES(X)
@@ -467,25 +501,92 @@ extern "C" void qkv_forward(bf16 *q, bf16 *k, bf16 *v, const bf16 *wq, const bf1
     X(1, 1) X(1, 2) X(1, 4) X(2, 1) X(2, 2) X(2, 4) X(3, 1) X(3, 2) X(4, 1) X(4, 2) X(5, 1) \
     X(6, 1) X(8, 1) X(10, 1) X(12, 1) X(16, 1) X(20, 1)
 
-extern "C" void gate_up_forward(bf16 *act, const bf16 *w_gate, const bf16 *w_up, const bf16 *x,
-                                int rows, int cols, bf16 *gate_tap, bf16 *up_tap,
-                                hipStream_t stream) {
-    if (!check_gemv("gate_up", w_gate, x, rows, cols) || !check_gemv("gate_up", w_up, x, rows, cols))
-        return;
+static void launch_gate_up(bf16 *act, const bf16 *w_gate, const bf16 *w_up, const bf16 *x,
+                           int rows, int cols, bf16 *gate_tap, bf16 *up_tap, const bf16 *norm_w,
+                           float eps, hipStream_t stream) {
     const int nc = pick_nc(cols / 8);
     const int rpw = pick_rpw(nc, rows, 1);
     const int waves = (rows + rpw - 1) / rpw;
     const int blocks = (waves + 3) / 4;
 #define X(NC_, RPW_)                                                                       \
     if (nc == NC_ && rpw == RPW_) {                                                        \
-        gate_up_kernel<NC_, RPW_><<<blocks, 256, 0, stream>>>(act, w_gate, w_up, x, rows,  \
-                                                             cols, gate_tap, up_tap);      \
+        if (norm_w)                                                                        \
+            gate_up_kernel<NC_, RPW_, true><<<blocks, 256, 0, stream>>>(                   \
+                act, w_gate, w_up, x, rows, cols, gate_tap, up_tap, norm_w, eps);          \
+        else                                                                               \
+            gate_up_kernel<NC_, RPW_><<<blocks, 256, 0, stream>>>(act, w_gate, w_up, x,    \
+                                                                 rows, cols, gate_tap, up_tap); \
         LAUNCH_OK();                                                                       \
         return;                                                                            \
     }
     GATE_UP_CASES(X)
 #undef X
     llm_fail("gate_up: no kernel for nc %d rpw %d", nc, rpw);
+}
+
+extern "C" void gate_up_forward(bf16 *act, const bf16 *w_gate, const bf16 *w_up, const bf16 *x,
+                                int rows, int cols, bf16 *gate_tap, bf16 *up_tap,
+                                hipStream_t stream) {
+    if (!check_gemv("gate_up", w_gate, x, rows, cols) || !check_gemv("gate_up", w_up, x, rows, cols))
+        return;
+    launch_gate_up(act, w_gate, w_up, x, rows, cols, gate_tap, up_tap, nullptr, 0.0f, stream);
+}
+
+// The fused forms: RMSNorm of x (one row) as the GEMV's prologue, summing the squares in the
+// order of rmsnorm_wave_kernel (lane l: chunks l, l+64, ..., then the wave tree), so the result
+// is rmsnorm_forward's. That kernel covers rows of up to 64 * 16 chunks (8192 columns), which
+// also fit one GEMV panel.
+static bool check_norm_fused(const char *name, const bf16 *norm_w, int cols) {
+    if (!norm_w) return llm_fail("%s: norm weights are NULL", name);
+    if (!aligned16(norm_w)) return llm_fail("%s: norm weights must be 16-byte aligned", name);
+    if ((cols / 8 + 63) / 64 > 16 || cols / 8 > 64 * pick_nc(cols / 8))
+        return llm_fail("%s: %d columns do not fit one panel (at most 8192)", name, cols);
+    return true;
+}
+
+extern "C" void rmsnorm_qkv_forward(bf16 *q, bf16 *k, bf16 *v, const bf16 *wq, const bf16 *wk,
+                                    const bf16 *wv, const bf16 *x, const bf16 *norm_w, float eps,
+                                    int q_rows, int kv_rows, int cols, hipStream_t stream) {
+    if (!check_gemv("rmsnorm_qkv", wq, x, q_rows, cols) ||
+        !check_gemv("rmsnorm_qkv", wk, x, kv_rows, cols) ||
+        !check_gemv("rmsnorm_qkv", wv, x, kv_rows, cols) ||
+        !check_norm_fused("rmsnorm_qkv", norm_w, cols))
+        return;
+    GemvArgs a = {};
+    a.seg[0] = {wq, q, q_rows, 0};
+    a.seg[1] = {wk, k, kv_rows, 0};
+    a.seg[2] = {wv, v, kv_rows, 0};
+    a.n_seg = 3;
+    a.x = x;
+    a.cols = cols;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    launch_gemv(a, EPI_PLAIN, stream);
+}
+
+extern "C" void rmsnorm_gemv_forward(bf16 *out, const bf16 *w, const bf16 *x, const bf16 *norm_w,
+                                     float eps, int rows, int cols, hipStream_t stream) {
+    if (!check_gemv("rmsnorm_gemv", w, x, rows, cols) ||
+        !check_norm_fused("rmsnorm_gemv", norm_w, cols))
+        return;
+    GemvArgs a = {};
+    a.seg[0] = {w, out, rows, 0};
+    a.n_seg = 1;
+    a.x = x;
+    a.cols = cols;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    launch_gemv(a, EPI_PLAIN, stream);
+}
+
+extern "C" void rmsnorm_gate_up_forward(bf16 *act, const bf16 *w_gate, const bf16 *w_up,
+                                        const bf16 *x, const bf16 *norm_w, float eps, int rows,
+                                        int cols, hipStream_t stream) {
+    if (!check_gemv("rmsnorm_gate_up", w_gate, x, rows, cols) ||
+        !check_gemv("rmsnorm_gate_up", w_up, x, rows, cols) ||
+        !check_norm_fused("rmsnorm_gate_up", norm_w, cols))
+        return;
+    launch_gate_up(act, w_gate, w_up, x, rows, cols, nullptr, nullptr, norm_w, eps, stream);
 }
 
 // ------------------------------------------------------------------------------------------

@@ -145,6 +145,51 @@ def test_gate_up(gpu, oracle, rows, cols):
     assert np.array_equal(host(act2), ea)
 
 
+# ---------------------------------------------------------------- RMSNorm fused into the GEMV
+
+FUSED_NORM_SHAPES = [(1024, 16, 8), (2560, 32, 8), (2048, 16, 8), (136, 3, 1),
+                     (8192, 2, 1)]
+
+
+@pytest.mark.parametrize("H,hq,hkv", FUSED_NORM_SHAPES)
+def test_rmsnorm_fused_gemvs(gpu, oracle, H, hq, hkv):
+    """The fused forms equal rmsnorm_forward followed by the plain launcher, bit for bit."""
+    ident(f"rmsnorm fused qkv/gemv/gate_up H={H} {hq}/{hkv}")
+    rng = np.random.default_rng(H + hq)
+    x = rand_bf16(rng, H, 1.0, 4.0)
+    g = rand_bf16(rng, H, 0.1, 1.0)
+    xn = oracle.rmsnorm(x[None], g, 1e-6, oracle.GPU_ORDER)[0]
+    wq = rand_bf16(rng, (hq * 128, H), 0.02)
+    wk = rand_bf16(rng, (hkv * 128, H), 0.02)
+    wv = rand_bf16(rng, (hkv * 128, H), 0.02)
+    q, k, v = (dev(np.zeros(n, np.uint16)) for n in (hq * 128, hkv * 128, hkv * 128))
+    gpu.rmsnorm_qkv_forward(q, k, v, dev(wq), dev(wk), dev(wv), dev(x), dev(g), 1e-6, hq * 128,
+                            hkv * 128, H)
+    eq, ek, ev = oracle.qkv(wq, wk, wv, xn, oracle.GPU_ORDER)
+    assert np.array_equal(host(q), eq)
+    assert np.array_equal(host(k), ek)
+    assert np.array_equal(host(v), ev)
+    rows = 3 * H + 5 if H <= 2560 else 1029
+    w = rand_bf16(rng, (rows, H), 0.02)
+    out = dev(np.zeros(rows, np.uint16))
+    gpu.rmsnorm_gemv_forward(out, dev(w), dev(x), dev(g), 1e-6, rows, H)
+    assert np.array_equal(host(out), oracle.gemv(w, xn, oracle.GPU_ORDER))
+    wg = rand_bf16(rng, (rows, H), 0.02)
+    act = dev(np.zeros(rows, np.uint16))
+    gpu.rmsnorm_gate_up_forward(act, dev(wg), dev(w), dev(x), dev(g), 1e-6, rows, H)
+    assert np.array_equal(host(act), oracle.gate_up(wg, w, xn, oracle.GPU_ORDER))
+
+
+def test_rmsnorm_fused_gemv_rejects_wide_rows(gpu):
+    """A row wider than 8192 columns is refused before any launch."""
+    H = 8200
+    x, g = dev(np.zeros(H, np.uint16)), dev(np.zeros(H, np.uint16))
+    w = dev(np.zeros((4, H), np.uint16))
+    out = dev(np.zeros(4, np.uint16))
+    with pytest.raises(gpu.LlmError, match="do not fit one panel"):
+        gpu.rmsnorm_gemv_forward(out, w, x, g, 1e-6, 4, H)
+
+
 # ---------------------------------------------------------------- SwiGLU
 
 @pytest.mark.parametrize("n", [65280, 4096 * 9728, 1001, 7])
