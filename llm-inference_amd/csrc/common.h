@@ -200,12 +200,11 @@ __device__ __forceinline__ void wave_amax(float &v, int &i) {
     }
 }
 
-// 2^n for n in [-126, 127].
-__device__ __forceinline__ float pow2i(int n) { return __uint_as_float((uint32_t)(n + 127) << 23); }
 
 // exp in fp32: k = rint(x log2 e); r = x - k ln2 (16-bit head of ln2 so k*hi and x - k*hi are
 // exact, then the tail); e^r by the degree-7 Taylor series as 1 + (r + r^2 q(r)); scaled by
-// 2^k in two steps so gradual underflow rounds once. Within 1 ulp of the correctly rounded
+// 2^k with one rounding (v_ldexp_f32; the same bits as p * 2^(k/2) * 2^(k - k/2), whose first
+// product is exact, so gradual underflow rounds once either way). Within 1 ulp of the correctly rounded
 // value for every fp32 input (checked exhaustively on the CPU against libm).
 __device__ __forceinline__ float exp_f32(float x) {
     if (x != x) return x;
@@ -223,10 +222,7 @@ __device__ __forceinline__ float exp_f32(float x) {
     float r2 = r * r;
     float t = fmaf(r2, q, r);
     float p = 1.0f + t;
-    int ki = (int)k;
-    int k1 = ki / 2;
-    int k2 = ki - k1;
-    return p * pow2i(k1) * pow2i(k2);
+    return __builtin_amdgcn_ldexpf(p, (int)k);
 }
 
 // sin and cos in double: k = rint(x 2/pi), r = x - k pi/2 with pi/2 in two 33-bit heads and a

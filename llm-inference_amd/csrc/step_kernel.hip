@@ -399,7 +399,6 @@ struct AttnSmem {
     float st[S::NMAX / 64][2];      // block max, block sum
     float gm[2];                    // global max, sum
     float quarter[PV_ROUND][4][D];  // PV partial of each (block, quarter) of a round
-    float out[D];                   // running sum over blocks
 };
 
 // One lane's 16 bytes of a KV-cache row. Rows written earlier in this launch (t >= pos0) were
@@ -601,7 +600,7 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
             const float M = wave_max(s);
             const float e = v ? exp_f32(s - M) : 0.0f;
             const float sum = wave_sum(e);
-            if (v) sm.sc[lane] = round_bf(exp_f32(s - M) / sum);
+            if (v) sm.sc[lane] = round_bf(e / sum);
         }
         __syncthreads();
     } else if (nb <= WAVES) {
@@ -670,24 +669,33 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
     }
     // PV in rounds of PV_ROUND blocks: wave w takes blocks c0 + w/4 + 2j and quarter w % 4 of
     // each (slots quarter*16 + it*4 + G); the quarters meet in order, the blocks are added in order
+    // by thread d < D, which keeps element d's running sum in a register
     const u32x4 vcur = sm.v[Lp];
+    float out_d = 0.0f;
     for (int c0 = 0; c0 < nb; c0 += PV_ROUND) {
         if (c0 > 0) load_v(c0);
 #pragma unroll
         for (int j = 0; j < PV_ROUND / 2; j++) {
             if (c0 + (w >> 2) + 2 * j >= nb) break;  // block past pos
+            // every slot of the block, with no branch around the probability reads: a slot past
+            // pos has value zeros and probability 0, and fma(0, 0, acc) is acc (acc starts at +0
+            // and an exact zero sum is +0, so acc is never -0)
+            float p[4];
+#pragma unroll
+            for (int it = 0; it < 4; it++) {
+                const int t = value_slot(c0, j, it);
+                const float pt = sm.sc[t];
+                p[it] = t < n ? pt : 0.0f;
+            }
             float acc[8];
 #pragma unroll
             for (int e = 0; e < 8; e++) acc[e] = 0.0f;
 #pragma unroll
             for (int it = 0; it < 4; it++) {
                 const int t = value_slot(c0, j, it);
-                if (t < n) {
-                    const float p = sm.sc[t];
-                    const u32x4 vt = t == pos ? vcur : vv[j][it];
+                const u32x4 vt = t == pos ? vcur : vv[j][it];
 #pragma unroll
-                    for (int e = 0; e < 8; e++) acc[e] = fmaf(p, elem(vt, e), acc[e]);
-                }
+                for (int e = 0; e < 8; e++) acc[e] = fmaf(p[it], elem(vt, e), acc[e]);
             }
             // the four slot groups (lanes 16 apart) summed with the pairing of butterfly_sum<16,
             // 64> (xor 16, then xor 32), reduce-scattered: the lane ends with elements d0, d0 + 1
@@ -704,6 +712,11 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
             qd[0] = two[0];
             qd[1] = two[1];
         }
+        const bool last = c0 + PV_ROUND >= nb;
+        // in the last round, the KV row this workgroup stored is complete before the sync, so
+        // before the output that later steps depend on is published (a later token of the
+        // launch reads the row from another workgroup)
+        if (last) __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         if (threadIdx.x < D) {
             const int d = threadIdx.x;
@@ -711,17 +724,12 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
                 const float part = ((sm.quarter[bi][0][d] + sm.quarter[bi][1][d]) +
                                     sm.quarter[bi][2][d]) +
                                    sm.quarter[bi][3][d];
-                sm.out[d] = c0 + bi == 0 ? part : sm.out[d] + part;
+                out_d = c0 + bi == 0 ? part : out_d + part;
             }
         }
-        __syncthreads();
+        if (!last) __syncthreads();  // the quarters are read before the next round rewrites them
     }
-    // the KV row this workgroup stored is complete before the output that later steps depend
-    // on is published (a later token of the launch reads it from another workgroup)
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x < D)
-        put_tagged_all<QD>(a.tattn, h * D + threadIdx.x, f2bf(sm.out[threadIdx.x]), tag_out);
+    if (threadIdx.x < D) put_tagged_all<QD>(a.tattn, h * D + threadIdx.x, f2bf(out_d), tag_out);
 }
 
 // ---------------------------------------------------------------- the step
