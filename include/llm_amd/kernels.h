@@ -61,8 +61,8 @@ void qk_norm_rope_forward(bf16 *q, bf16 *k, const bf16 *v, const bf16 *q_norm_w,
 
 /* src/kernels.cuh:22-24. Decode attention of the query at position *d_pos over cache rows
  * 0..*d_pos, GQA kv_head = h / (n_heads / n_kv_heads). scores bf16(bf16(q.k) * scale), softmax
- * probabilities rounded to bf16, out = bf16(sum p v). `att` is fp32 scratch of at least
- * attention_workspace_floats(n_heads, head_dim, max_seq) floats: the reference's
+ * probabilities rounded to bf16, out = bf16(sum p v). `att` is 16-byte aligned fp32 scratch of
+ * at least attention_workspace_floats(n_heads, head_dim, max_seq) floats: the reference's
  * [n_heads, max_seq] score rows followed by the split-softmax block statistics and partial
  * outputs. head_dim in {64, 128, 256}; n_heads / n_kv_heads in {1, 2, 4, 8}. */
 void attention_forward(bf16 *out, const bf16 *q, const bf16 *key_cache, const bf16 *value_cache,

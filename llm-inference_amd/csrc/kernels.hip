@@ -232,15 +232,19 @@ struct GemvArgs {
 
 // The fused RMSNorm prologue of a one-panel GEMV: the wave's input chunks (lane l: chunks
 // l + 64k, the layout of rmsnorm_wave_kernel<NC>) normalised in registers with that kernel's
-// arithmetic, so the GEMV sees exactly the bf16 vector rmsnorm_forward would have written.
+// arithmetic, so the GEMV sees exactly the bf16 vector rmsnorm_forward would have written. The
+// gamma chunks are requested with the input, before the weight rows, and the arithmetic runs
+// after the weight requests: loads complete in order, so it waits for the input and gamma only.
 template <int NC>
-__device__ __forceinline__ void norm_chunks(u32x4 (&xv)[NC], const bf16 *gamma, int cols, float eps) {
+__device__ __forceinline__ void norm_gamma_load(const bf16 *gamma, int cols, u32x4 (&gv)[NC]) {
     const int lane = tid_x() & 63;
     const __amdgpu_buffer_rsrc_t gr =
         __builtin_amdgcn_make_buffer_rsrc((void *)gamma, (short)0, cols * 2, BUFFER_FLAGS);
-    u32x4 gv[NC];
 #pragma unroll
     for (int k = 0; k < NC; k++) gv[k] = __builtin_amdgcn_raw_buffer_load_b128(gr, 16 * (lane + 64 * k), 0, 0);
+}
+template <int NC>
+__device__ __forceinline__ void norm_apply(u32x4 (&xv)[NC], const u32x4 (&gv)[NC], int cols, float eps) {
     float acc = 0.0f;
 #pragma unroll
     for (int k = 0; k < NC; k++) acc = dot8(xv[k], xv[k], acc);
@@ -262,6 +266,12 @@ enum { EPI_PLAIN = 0, EPI_RESID = 1 };
 // then gives every lane each row's sum and lane i stores row row0+i.
 template <int NC, int RPW, int EPI, bool NORM = false>
 __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+    // Wide rows (NC >= 10: over 4096 columns) take the input through LDS: the workgroup loads
+    // each panel of x once instead of once per wave, which at one row per wave would double the
+    // L2-to-CU traffic of the weight stream.
+    constexpr bool XLDS = NC >= 10 && !NORM;
+    constexpr int XT = XLDS ? (64 * NC + 255) / 256 : 1;  // x chunks per thread and panel
+    __shared__ u32x4 xs[XLDS ? 64 * NC : 1];
     const int lane = threadIdx.x & 63;
     // wave-uniform (scalar), so the per-row buffer descriptors below are scalar too
     const int wave = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -273,7 +283,10 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     const int rows = si == 0 ? a.seg[0].rows : si == 1 ? a.seg[1].rows : a.seg[2].rows;
     const int wb = si == 0 ? a.seg[0].wave_begin : si == 1 ? a.seg[1].wave_begin : a.seg[2].wave_begin;
     const int row0 = (wave - wb) * RPW;
-    if (row0 >= rows) return;
+    // with XLDS every wave takes part in the workgroup's syncs; a wave without rows loads
+    // nothing (zero-size row buffers) and stores nothing
+    const bool active = row0 < rows;
+    if (!XLDS && !active) return;
     const int cols = a.cols;
     const int n_chunks = cols >> 3;
     const __amdgpu_buffer_rsrc_t xr =
@@ -284,27 +297,47 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     for (int c0 = 0; c0 < n_chunks; c0 += 64 * NC) {
         u32x4 wv[RPW][NC];
         u32x4 xv[NC];
+        u32x4 xt[XT];
+        if constexpr (XLDS) {
 #pragma unroll
-        for (int k = 0; k < NC; k++)
-            xv[k] = __builtin_amdgcn_raw_buffer_load_b128(xr, 16 * (c0 + lane + 64 * k), 0, 0);
-        if constexpr (NORM) norm_chunks<NC>(xv, a.norm_w, cols, a.eps);  // one panel (host check)
+            for (int j = 0; j < XT; j++)
+                xt[j] = __builtin_amdgcn_raw_buffer_load_b128(
+                    xr, 16 * (c0 + (int)threadIdx.x + 256 * j), 0, 0);
+        } else {
+#pragma unroll
+            for (int k = 0; k < NC; k++)
+                xv[k] = __builtin_amdgcn_raw_buffer_load_b128(xr, 16 * (c0 + lane + 64 * k), 0, 0);
+        }
+        u32x4 gm[NC];  // one panel when NORM (host check)
+        if constexpr (NORM) norm_gamma_load<NC>(a.norm_w, cols, gm);
 #pragma unroll
         for (int i = 0; i < RPW; i++) {
             // the row as a buffer: chunks past its end read as zeros with no branch around the
             // loads, so each chunk's FMAs wait only for that chunk's load
             const int r = min(row0 + i, rows - 1);
             const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-                (void *)(w + (size_t)r * cols), (short)0, cols * 2, BUFFER_FLAGS);
+                (void *)(w + (size_t)r * cols), (short)0, active ? cols * 2 : 0, BUFFER_FLAGS);
 #pragma unroll
             for (int k = 0; k < NC; k++)
                 wv[i][k] = __builtin_amdgcn_raw_buffer_load_b128(rs, 16 * (c0 + lane + 64 * k), 0,
                                                                  BUFFER_NT);
         }
+        if constexpr (XLDS) {
+            if (c0 > 0) __syncthreads();  // every wave has read the previous panel
+#pragma unroll
+            for (int j = 0; j < XT; j++)
+                if ((int)threadIdx.x + 256 * j < 64 * NC) xs[threadIdx.x + 256 * j] = xt[j];
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < NC; k++) xv[k] = xs[lane + 64 * k];
+        }
+        if constexpr (NORM) norm_apply<NC>(xv, gm, cols, a.eps);
 #pragma unroll
         for (int i = 0; i < RPW; i++)
 #pragma unroll
             for (int k = 0; k < NC; k++) acc[i] = dot8(wv[i][k], xv[k], acc[i]);
     }
+    if (!active) return;
     float mine = 0.0f;
 #pragma unroll
     for (int i = 0; i < RPW; i++) {
@@ -347,7 +380,8 @@ __global__ __launch_bounds__(256) void gate_up_kernel(bf16 *act, const bf16 *wg,
 #pragma unroll
         for (int k = 0; k < NC; k++)
             xv[k] = __builtin_amdgcn_raw_buffer_load_b128(xr, 16 * (c0 + lane + 64 * k), 0, 0);
-        if constexpr (NORM) norm_chunks<NC>(xv, norm_w, cols, eps);  // one panel (host check)
+        u32x4 gm[NC];  // one panel when NORM (host check)
+        if constexpr (NORM) norm_gamma_load<NC>(norm_w, cols, gm);
 #pragma unroll
         for (int i = 0; i < RPW; i++) {
             const size_t r = (size_t)min(row0 + i, rows - 1);
@@ -362,6 +396,7 @@ __global__ __launch_bounds__(256) void gate_up_kernel(bf16 *act, const bf16 *wg,
                 uv[i][k] = __builtin_amdgcn_raw_buffer_load_b128(ru, off, 0, BUFFER_NT);
             }
         }
+        if constexpr (NORM) norm_apply<NC>(xv, gm, cols, eps);
 #pragma unroll
         for (int i = 0; i < RPW; i++)
 #pragma unroll
@@ -872,9 +907,16 @@ struct AttnArgs {
 
 static size_t ceil_div(size_t a, size_t b) { return (a + b - 1) / b; }
 
+// Workspace layout: scores [n_heads, max_seq], stats [n_heads, max_blocks, 2], then (from a
+// 16-byte boundary) partials [n_heads, max_blocks, D].
+static size_t attention_partial_offset(int n_heads, int max_seq) {
+    const size_t mb = ceil_div((size_t)max_seq, ATT_B);
+    return ceil_div((size_t)n_heads * max_seq + (size_t)n_heads * mb * 2, 4) * 4;
+}
+
 extern "C" size_t attention_workspace_floats(int n_heads, int head_dim, int max_seq) {
     const size_t mb = ceil_div((size_t)max_seq, ATT_B);
-    return (size_t)n_heads * max_seq + (size_t)n_heads * mb * (2 + (size_t)head_dim);
+    return attention_partial_offset(n_heads, max_seq) + (size_t)n_heads * mb * head_dim;
 }
 
 // Pass 1, per (block of 64 positions, kv head): scores of the REP query heads sharing the kv
@@ -1052,27 +1094,46 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnArgs a) {
     }
 }
 
-// Pass 3: out = bf16(block partials added in block order). The additions are sequential, the
-// loads are not: 16 partials per thread are requested before any is added.
+// Pass 3: out = bf16(block partials added in block order), one workgroup per query head. The
+// additions are sequential, the loads are not: the head's partials are staged in LDS by all 256
+// threads (every 16-byte load of a chunk of CB blocks in flight at once), then thread d adds
+// column d in block order, 16 LDS reads at a time.
 template <int D>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
-    constexpr int BATCH = 16;
+    constexpr int CB = 32768 / D;  // blocks per LDS chunk (128 KB: one chunk up to 16384 positions at D = 128)
+    __shared__ float part[CB * D];
     const int h = blockIdx.x;
     const int n = *a.d_pos + 1;
     const int nb = (n + ATT_B - 1) / ATT_B;
-    for (int d = threadIdx.x; d < D; d += blockDim.x) {
-        const float *p = a.partial + (size_t)h * a.max_blocks * D + d;
-        float acc = p[0];
-        for (int b0 = 1; b0 < nb; b0 += BATCH) {
-            float v[BATCH];
+    const float *src = a.partial + (size_t)h * a.max_blocks * D;
+    float acc = 0.0f;
+    for (int b0 = 0; b0 < nb; b0 += CB) {
+        const int cnt = min(CB, nb - b0);
+        if (b0 > 0) __syncthreads();  // the previous chunk has been added
+        const u32x4 *s4 = (const u32x4 *)(src + (size_t)b0 * D);
+        constexpr int PER = CB * D / 4 / 256;  // 16-byte loads per thread for a full chunk
+        const int n4 = cnt * D / 4;
+        u32x4 v4[PER];
 #pragma unroll
-            for (int j = 0; j < BATCH; j++) v[j] = p[(size_t)min(b0 + j, nb - 1) * D];
+        for (int j = 0; j < PER; j++) v4[j] = s4[min((int)threadIdx.x + 256 * j, n4 - 1)];
 #pragma unroll
-            for (int j = 0; j < BATCH; j++)
-                if (b0 + j < nb) acc = acc + v[j];
+        for (int j = 0; j < PER; j++)
+            if ((int)threadIdx.x + 256 * j < n4) ((u32x4 *)part)[threadIdx.x + 256 * j] = v4[j];
+        __syncthreads();
+        if (threadIdx.x < D) {
+            // 16 LDS reads in flight, then their additions in order
+            const int d = threadIdx.x;
+            for (int j0 = 0; j0 < cnt; j0 += 16) {
+                float v[16];
+#pragma unroll
+                for (int j = 0; j < 16; j++) v[j] = part[min(j0 + j, cnt - 1) * D + d];
+#pragma unroll
+                for (int j = 0; j < 16; j++)
+                    if (j0 + j < cnt) acc = (b0 + j0 + j == 0) ? v[j] : acc + v[j];
+            }
         }
-        a.out[(size_t)h * D + d] = (bf16)f2bf(acc);
     }
+    if (threadIdx.x < D) a.out[(size_t)h * D + threadIdx.x] = (bf16)f2bf(acc);
 }
 
 template <int D, int REP>
@@ -1081,36 +1142,25 @@ static void launch_attention_t(const AttnArgs &a, int grid, hipStream_t stream) 
     if (!LAUNCH_OK()) return;
     attn_pv_kernel<D, REP><<<grid, 256, 0, stream>>>(a);
     if (!LAUNCH_OK()) return;
-    attn_combine_kernel<D><<<a.n_heads, D < 256 ? D : 256, 0, stream>>>(a);
+    attn_combine_kernel<D><<<a.n_heads, 256, 0, stream>>>(a);
     LAUNCH_OK();
 }
 
-extern "C" void attention_forward(bf16 *out, const bf16 *q, const bf16 *key_cache,
-                                  const bf16 *value_cache, float *att, int n_heads, int n_kv_heads,
-                                  int head_dim, const int *d_pos, int max_seq, float scale,
-                                  hipStream_t stream) {
-    if (head_dim != 64 && head_dim != 128 && head_dim != 256) {
-        llm_fail("attention: head_dim %d is not 64, 128 or 256", head_dim);
-        return;
-    }
-    if (n_kv_heads <= 0 || n_heads % n_kv_heads != 0) {
-        llm_fail("attention: n_heads %d is not a multiple of n_kv_heads %d", n_heads, n_kv_heads);
-        return;
-    }
+static bool attention_args(AttnArgs &a, int &grid, bf16 *out, const bf16 *q,
+                           const bf16 *key_cache, const bf16 *value_cache, float *att,
+                           int n_heads, int n_kv_heads, int head_dim, const int *d_pos,
+                           int max_seq, float scale) {
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+        return llm_fail("attention: head_dim %d is not 64, 128 or 256", head_dim);
+    if (n_kv_heads <= 0 || n_heads % n_kv_heads != 0)
+        return llm_fail("attention: n_heads %d is not a multiple of n_kv_heads %d", n_heads,
+                        n_kv_heads);
     const int rep = n_heads / n_kv_heads;
-    if (rep != 1 && rep != 2 && rep != 4 && rep != 8) {
-        llm_fail("attention: n_heads / n_kv_heads = %d is not 1, 2, 4 or 8", rep);
-        return;
-    }
-    if (max_seq <= 0) {
-        llm_fail("attention: max_seq %d must be positive", max_seq);
-        return;
-    }
-    if (!aligned16(q) || !aligned16(key_cache) || !aligned16(value_cache)) {
-        llm_fail("attention: q and the caches must be 16-byte aligned");
-        return;
-    }
-    AttnArgs a;
+    if (rep != 1 && rep != 2 && rep != 4 && rep != 8)
+        return llm_fail("attention: n_heads / n_kv_heads = %d is not 1, 2, 4 or 8", rep);
+    if (max_seq <= 0) return llm_fail("attention: max_seq %d must be positive", max_seq);
+    if (!aligned16(q) || !aligned16(key_cache) || !aligned16(value_cache) || !aligned16(att))
+        return llm_fail("attention: q, the caches and att must be 16-byte aligned");
     a.out = out;
     a.q = q;
     a.kc = key_cache;
@@ -1118,14 +1168,30 @@ extern "C" void attention_forward(bf16 *out, const bf16 *q, const bf16 *key_cach
     a.max_blocks = (int)ceil_div((size_t)max_seq, ATT_B);
     a.scores = att;
     a.stats = att + (size_t)n_heads * max_seq;
-    a.partial = a.stats + (size_t)n_heads * a.max_blocks * 2;
+    a.partial = att + attention_partial_offset(n_heads, max_seq);
     a.d_pos = d_pos;
     a.n_heads = n_heads;
     a.n_kv_heads = n_kv_heads;
     a.max_seq = max_seq;
     a.scale = scale;
-    long items = (long)a.max_blocks * n_kv_heads;
-    const int grid = (int)(items < 1024 ? items : 1024);
+    // one workgroup per (block, kv head) of the longest history, so every item of a step runs in
+    // the same wave of workgroups (a fixed cap made the last few items of a long history a second
+    // wave that doubled the kernel time); items beyond the current history exit at once
+    const long items = (long)a.max_blocks * n_kv_heads;
+    grid = (int)(items < 8192 ? items : 8192);
+    return true;
+}
+
+extern "C" void attention_forward(bf16 *out, const bf16 *q, const bf16 *key_cache,
+                                  const bf16 *value_cache, float *att, int n_heads, int n_kv_heads,
+                                  int head_dim, const int *d_pos, int max_seq, float scale,
+                                  hipStream_t stream) {
+    AttnArgs a;
+    int grid = 0;
+    if (!attention_args(a, grid, out, q, key_cache, value_cache, att, n_heads, n_kv_heads,
+                        head_dim, d_pos, max_seq, scale))
+        return;
+    const int rep = n_heads / n_kv_heads;
 #define ATT(D_, R_)                                    \
     if (head_dim == D_ && rep == R_) {                 \
         launch_attention_t<D_, R_>(a, grid, stream);   \

@@ -38,16 +38,39 @@ __device__ __forceinline__ void rope_table(int pos, Table inv_freq,
     }
 }
 
-// RMSNorm of the head (weight chunks wa/wb), then the rotation. Outputs: the normed chunks
-// (ya/yb, for taps) and the rotated chunks (oa/ob). Every lane of the wave must call this
-// (it shuffles); lanes of an absent head pass zeros and ignore the results.
+// The table entries of rotation pairs 8L .. 8L+7 (a lane's chunk), fetched from the lanes that
+// computed them. Every lane of the wave must call this (it shuffles).
 template <int D>
-__device__ __forceinline__ void norm_rope(const u32x4 &xa, const u32x4 &xb, const u32x4 &wa,
-                                          const u32x4 &wb, float eps,
-                                          const float (&cs)[RopeShape<D>::NJ],
-                                          const float (&sn)[RopeShape<D>::NJ], int L, u32x4 &ya_out,
-                                          u32x4 &yb_out, u32x4 &oa_out, u32x4 &ob_out) {
-    constexpr int LH = RopeShape<D>::LH, NJ = RopeShape<D>::NJ;
+__device__ __forceinline__ void rope_fetch(const float (&cs)[RopeShape<D>::NJ],
+                                           const float (&sn)[RopeShape<D>::NJ], int L,
+                                           float (&c)[8], float (&s)[8]) {
+    constexpr int NJ = RopeShape<D>::NJ;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const int j = 8 * L + e;
+        c[e] = __shfl(cs[0], j & 63);
+        s[e] = __shfl(sn[0], j & 63);
+#pragma unroll
+        for (int m = 1; m < NJ; m++) {
+            const float cm = __shfl(cs[m], j & 63), sm = __shfl(sn[m], j & 63);
+            if ((j >> 6) == m) {
+                c[e] = cm;
+                s[e] = sm;
+            }
+        }
+    }
+}
+
+// RMSNorm of the head (weight chunks wa/wb), then the rotation with the lane's table entries
+// c/s (rope_fetch). Outputs: the normed chunks (ya/yb, for taps) and the rotated chunks
+// (oa/ob). The lanes of a head must call this together (the sum of squares is a lane tree);
+// lanes of an absent head pass zeros and ignore the results.
+template <int D>
+__device__ __forceinline__ void norm_rope_with(const u32x4 &xa, const u32x4 &xb, const u32x4 &wa,
+                                               const u32x4 &wb, float eps, const float (&c)[8],
+                                               const float (&s)[8], u32x4 &ya_out, u32x4 &yb_out,
+                                               u32x4 &oa_out, u32x4 &ob_out) {
+    constexpr int LH = RopeShape<D>::LH;
     float acc = dot8(xa, xa, 0.0f);
     acc = dot8(xb, xb, acc);
     const float total = group_sum<LH>(acc);
@@ -61,20 +84,10 @@ __device__ __forceinline__ void norm_rope(const u32x4 &xa, const u32x4 &xb, cons
     float oa[8], ob[8];
 #pragma unroll
     for (int e = 0; e < 8; e++) {
-        const int j = 8 * L + e;
-        float c = __shfl(cs[0], j & 63), s = __shfl(sn[0], j & 63);
-#pragma unroll
-        for (int m = 1; m < NJ; m++) {
-            const float cm = __shfl(cs[m], j & 63), sm = __shfl(sn[m], j & 63);
-            if ((j >> 6) == m) {
-                c = cm;
-                s = sm;
-            }
-        }
-        const float a_cos = round_bf(ya[e] * c);
-        const float b_sin = round_bf(yb[e] * s);
-        const float b_cos = round_bf(yb[e] * c);
-        const float a_sin = round_bf(ya[e] * s);
+        const float a_cos = round_bf(ya[e] * c[e]);
+        const float b_sin = round_bf(yb[e] * s[e]);
+        const float b_cos = round_bf(yb[e] * c[e]);
+        const float a_sin = round_bf(ya[e] * s[e]);
         oa[e] = a_cos - b_sin;
         ob[e] = b_cos + a_sin;
     }
@@ -82,6 +95,18 @@ __device__ __forceinline__ void norm_rope(const u32x4 &xa, const u32x4 &xb, cons
     yb_out = u32x4{pack2(yb[0], yb[1]), pack2(yb[2], yb[3]), pack2(yb[4], yb[5]), pack2(yb[6], yb[7])};
     oa_out = u32x4{pack2(oa[0], oa[1]), pack2(oa[2], oa[3]), pack2(oa[4], oa[5]), pack2(oa[6], oa[7])};
     ob_out = u32x4{pack2(ob[0], ob[1]), pack2(ob[2], ob[3]), pack2(ob[4], ob[5]), pack2(ob[6], ob[7])};
+}
+
+// rope_fetch + norm_rope_with. Every lane of the wave must call this (it shuffles).
+template <int D>
+__device__ __forceinline__ void norm_rope(const u32x4 &xa, const u32x4 &xb, const u32x4 &wa,
+                                          const u32x4 &wb, float eps,
+                                          const float (&cs)[RopeShape<D>::NJ],
+                                          const float (&sn)[RopeShape<D>::NJ], int L, u32x4 &ya_out,
+                                          u32x4 &yb_out, u32x4 &oa_out, u32x4 &ob_out) {
+    float c[8], s[8];
+    rope_fetch<D>(cs, sn, L, c, s);
+    norm_rope_with<D>(xa, xb, wa, wb, eps, c, s, ya_out, yb_out, oa_out, ob_out);
 }
 
 }  // namespace llm

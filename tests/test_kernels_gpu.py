@@ -298,7 +298,7 @@ def test_qk_norm_rope_rows_sweep(gpu, oracle):
 
 @pytest.mark.parametrize("hq,hkv,pos", [(16, 8, 0), (16, 8, 4), (16, 8, 63), (16, 8, 64),
                                         (16, 8, 260), (32, 8, 4095), (32, 8, 8447), (8, 8, 100),
-                                        (8, 1, 130)])
+                                        (8, 1, 130), (3, 3, 4100)])
 def test_attention(gpu, oracle, hq, hkv, pos):
     ident(f"attention {hq}/{hkv} pos{pos}")
     rng = np.random.default_rng(hq * 10000 + pos)
