@@ -208,6 +208,13 @@ def test_swiglu(gpu, oracle, n):
     assert np.array_equal(y, oracle.swiglu(g, u, oracle.GPU_ORDER))
     s_exact = oracle.swiglu(g, bf16_bits(np.ones(g.size)), oracle.EXACT)
     assert within_one_ulp_then_scale(y, s_exact, u).all()
+    if n == 65280:
+        # u = 1: the rounded SiLU itself, for every finite bf16 gate value (the kernel's fast
+        # estimate must round like the precise formula everywhere)
+        ones = bf16_bits(np.ones(g.size))
+        act1 = dev(np.zeros(g.size, np.uint16))
+        gpu.swiglu_forward(act1, dev(g), dev(ones), g.size)
+        assert np.array_equal(host(act1), oracle.swiglu(g, ones, oracle.GPU_ORDER))
 
 
 # ---------------------------------------------------------------- QK-norm + RoPE + KV write
