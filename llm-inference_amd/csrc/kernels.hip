@@ -739,7 +739,7 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(RopeArgs a) {
     constexpr int HALF = D / 2;
     constexpr int NJ = (HALF + 63) / 64;
     const int lane = threadIdx.x & 63;
-    const int wave = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int wave = blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int per_token = a.qg + a.kg + a.vg;
     const int t = wave / per_token;
     if (t >= a.n_tokens) return;
@@ -760,34 +760,37 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(RopeArgs a) {
         return;
     }
     const bool is_k = item >= a.qg;
-    const int h = (is_k ? item - a.qg : item) * HPW + hg;
-    const bool valid = h < (is_k ? a.n_kv_heads : a.n_heads);
-    const size_t off = (size_t)t * (is_k ? kv_dim : q_dim) + (size_t)h * D;
-    bf16 *x = (is_k ? a.k : a.q) + off;
-    const bf16 *w = is_k ? a.kn : a.qn;
+    // the wave's heads h0 .. h0 + HPW - 1 (those that exist) as one buffer, so the descriptor is
+    // wave-uniform: loads past the last head read zeros and stores there are dropped; the
+    // loads go out before the RoPE table is computed, which then overlaps them
+    const int h0 = (is_k ? item - a.qg : item) * HPW;
+    const int n_h = min(HPW, (is_k ? a.n_kv_heads : a.n_heads) - h0);
+    const size_t off = (size_t)t * (is_k ? kv_dim : q_dim) + (size_t)h0 * D;
     bf16 *tap = is_k ? a.k_tap : a.q_tap;
-
+    auto heads = [&](bf16 *base) {
+        return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, n_h * D * 2, BUFFER_FLAGS);
+    };
+    const __amdgpu_buffer_rsrc_t xr = heads((is_k ? a.k : a.q) + off);
+    const int oa = hg * D * 2 + 16 * L, ob = oa + 2 * HALF;
+    const u32x4 xa = __builtin_amdgcn_raw_buffer_load_b128(xr, oa, 0, BUFFER_NT);
+    const u32x4 xb = __builtin_amdgcn_raw_buffer_load_b128(xr, ob, 0, BUFFER_NT);
+    const bf16 *w = is_k ? a.kn : a.qn;
+    const u32x4 wa = ld16(w + 8 * L), wb = ld16(w + HALF + 8 * L);
     float cs[NJ], sn[NJ];
     rope_table<D>(pos, a.inv_freq, cs, sn);
-    u32x4 xa = {0, 0, 0, 0}, xb = {0, 0, 0, 0};
-    if (valid) {
-        xa = ld16(x + 8 * L);
-        xb = ld16(x + HALF + 8 * L);
-    }
-    const u32x4 wa = ld16(w + 8 * L), wb = ld16(w + HALF + 8 * L);
     u32x4 ya, yb, va, vb;
     norm_rope<D>(xa, xb, wa, wb, a.eps, cs, sn, L, ya, yb, va, vb);
-    if (valid && tap) {
-        st16(tap + off + 8 * L, ya);
-        st16(tap + off + HALF + 8 * L, yb);
+    if (tap) {
+        const __amdgpu_buffer_rsrc_t tr = heads(tap + off);
+        __builtin_amdgcn_raw_buffer_store_b128(ya, tr, oa, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b128(yb, tr, ob, 0, 0);
     }
-    if (valid) {
-        st16(x + 8 * L, va);
-        st16(x + HALF + 8 * L, vb);
-        if (is_k) {
-            st16(a.kc + slot + h * D + 8 * L, va);
-            st16(a.kc + slot + h * D + HALF + 8 * L, vb);
-        }
+    __builtin_amdgcn_raw_buffer_store_b128(va, xr, oa, 0, BUFFER_NT);
+    __builtin_amdgcn_raw_buffer_store_b128(vb, xr, ob, 0, BUFFER_NT);
+    if (is_k) {
+        const __amdgpu_buffer_rsrc_t cr = heads(a.kc + slot + (size_t)h0 * D);
+        __builtin_amdgcn_raw_buffer_store_b128(va, cr, oa, 0, BUFFER_NT);
+        __builtin_amdgcn_raw_buffer_store_b128(vb, cr, ob, 0, BUFFER_NT);
     }
 }
 
