@@ -123,9 +123,9 @@ typedef struct {
 
 /* How capture_graph prepares the step. STEP_AUTO: the persistent step kernel (one cooperative
  * launch per forward; generate_greedy runs all its tokens in one launch) when the shapes have a
- * specialisation, else a hipGraph of the per-layer
- * kernels. STEP_GRAPH: always the hipGraph. STEP_PERSISTENT: the persistent kernel or an
- * error. */
+ * specialisation and the hidden size is at most 2048 (Qwen3-0.6B and 1.7B, where it is the
+ * faster step), else a hipGraph of the per-layer kernels. STEP_GRAPH: always the hipGraph.
+ * STEP_PERSISTENT: the persistent kernel (also at 4B) or an error. */
 enum { STEP_AUTO = 0, STEP_GRAPH = 1, STEP_PERSISTENT = 2 };
 
 /* src/loader.cu:105-139 (config.json, generation_config.json) */

@@ -92,6 +92,10 @@ __device__ __forceinline__ int tid_x() {
     return t;
 }
 
+// The wave's index in the workgroup as a wave-uniform (scalar) value, so branches on it are
+// scalar branches and not per-lane masks.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(tid_x() >> 6); }
+
 // The value of lane (lane ^ S), S a power of two below 64, without an LDS address: DPP
 // quad_perm for 1 and 2, ds_swizzle in bitmask mode (and 0x1f, xor S) for 4..16, and
 // v_permlane32_swap of the register with itself for 32 (afterwards the first result holds the

@@ -283,7 +283,9 @@ extern "C" void capture_graph(const Config *cfg, const Weights *w, RunState *s) 
         s->graph = nullptr;
     }
     s->persistent = 0;
-    if (s->step_mode != STEP_GRAPH && step_kernel_supported(cfg, s->max_seq)) {
+    const bool want = s->step_mode == STEP_PERSISTENT ||
+                      (s->step_mode == STEP_AUTO && step_kernel_preferred(cfg));
+    if (want && step_kernel_supported(cfg, s->max_seq)) {
         prepare_persistent(cfg, w, s);
         return;
     }

@@ -50,5 +50,7 @@ struct StepWorkspace {
 
 size_t step_workspace_bytes(const Config *cfg);
 bool step_kernel_supported(const Config *cfg, int max_seq);
+// Whether STEP_AUTO takes the step kernel (where it is supported) over the hipGraph step.
+bool step_kernel_preferred(const Config *cfg);
 int step_kernel_grid();
 bool step_kernel_launch(const Config *cfg, const StepArgs &args, int grid, hipStream_t stream);
