@@ -105,6 +105,13 @@ void rmsnorm_gate_up_forward(bf16 *act, const bf16 *w_gate, const bf16 *w_up, co
                              const bf16 *norm_w, float eps, int rows, int cols,
                              hipStream_t stream);
 
+/* Measurement helper, no counterpart in the reference: the streaming ceiling that the
+ * bandwidth-bound kernels are compared with. mode 0: read n_bytes of a (dst receives one 32-bit
+ * word per thread: at least 1 MiB); mode 1: copy n_bytes from a to dst; mode 2: dst = a ^ b over
+ * n_bytes each (two streams in, one out, as SwiGLU). n_bytes % 16 == 0, 16-byte aligned. */
+void hbm_stream_probe(void *dst, const void *a, const void *b, size_t n_bytes, int mode,
+                      hipStream_t stream);
+
 /* Floats attention_forward needs in `att` for these sizes. */
 size_t attention_workspace_floats(int n_heads, int head_dim, int max_seq);
 

@@ -327,6 +327,31 @@ def test_attention(gpu, oracle, hq, hkv, pos):
                                              oracle.EXACT)).max() <= 2
 
 
+def test_hbm_stream_probe(gpu):
+    """The ceiling probe's three modes compute what they claim (copy, xor of two streams, and a
+    per-thread xor of the read chunks), including a length that is not a multiple of the grid."""
+    import torch
+    ident("hbm_stream_probe")
+    n16 = 1024 * 256 * 4 * 3 + 5  # grid-stride remainder for the read mode
+    a = torch.randint(0, 1 << 30, (n16 * 4,), dtype=torch.int32, device="cuda")
+    b = torch.randint(0, 1 << 30, (n16 * 4,), dtype=torch.int32, device="cuda")
+    dst = torch.zeros(n16 * 4, dtype=torch.int32, device="cuda")
+    gpu.hbm_stream_probe(dst, a, None, n16 * 16, 1)
+    assert torch.equal(dst, a)
+    gpu.hbm_stream_probe(dst, a, b, n16 * 16, 2)
+    assert torch.equal(dst, a ^ b)
+    out = torch.zeros(1 << 18, dtype=torch.int32, device="cuda")
+    gpu.hbm_stream_probe(out, a, None, n16 * 16, 0)
+    # thread b * 256 + i xors chunks b * 1024 + i + 256 u + (1024 * 1024) j (all four words)
+    chunks = a.view(n16, 4).cpu().numpy().astype(np.uint32)
+    words = np.bitwise_xor.reduce(chunks, axis=1)
+    c = np.arange(n16) % (1024 * 1024)
+    thread = (c // 1024) * 256 + c % 256
+    expect = np.zeros(1 << 18, np.uint32)
+    np.bitwise_xor.at(expect, thread, words)
+    assert np.array_equal(out.cpu().numpy().astype(np.uint32), expect)
+
+
 # ---------------------------------------------------------------- argmax
 
 def test_argmax(gpu, oracle):
