@@ -102,3 +102,32 @@ def within_one_ulp_then_scale(y, n_exact, scale):
     for k in (-1, 0, 1):
         ok |= y == bf16_bits(bf16_vals(bf16_step(n_exact, k)) * s)
     return ok
+
+
+# The small Qwen3 of the end-to-end tests and of the HF golden fixture (tests/golden): seeded
+# N(0, 0.02) matrices and 1 + N(0, 0.1) norm weights, as bf16 bits, in the checkpoint's names.
+SMALL = dict(hidden_size=256, intermediate_size=512, n_layers=2, n_heads=4, n_kv_heads=2,
+             head_dim=128, vocab_size=1000)
+
+
+def small_weights(seed=0):
+    rng = np.random.default_rng(seed)
+    c = SMALL
+    H, I, D = c["hidden_size"], c["intermediate_size"], c["head_dim"]
+    qd, kvd = c["n_heads"] * D, c["n_kv_heads"] * D
+    w = {"model.embed_tokens.weight": rand_bf16(rng, (c["vocab_size"], H), 0.02)}
+    for l in range(c["n_layers"]):
+        p = f"model.layers.{l}."
+        w[p + "input_layernorm.weight"] = rand_bf16(rng, H, 0.1, 1.0)
+        w[p + "self_attn.q_proj.weight"] = rand_bf16(rng, (qd, H), 0.02)
+        w[p + "self_attn.k_proj.weight"] = rand_bf16(rng, (kvd, H), 0.02)
+        w[p + "self_attn.v_proj.weight"] = rand_bf16(rng, (kvd, H), 0.02)
+        w[p + "self_attn.q_norm.weight"] = rand_bf16(rng, D, 0.1, 1.0)
+        w[p + "self_attn.k_norm.weight"] = rand_bf16(rng, D, 0.1, 1.0)
+        w[p + "self_attn.o_proj.weight"] = rand_bf16(rng, (H, qd), 0.02)
+        w[p + "post_attention_layernorm.weight"] = rand_bf16(rng, H, 0.1, 1.0)
+        w[p + "mlp.gate_proj.weight"] = rand_bf16(rng, (I, H), 0.02)
+        w[p + "mlp.up_proj.weight"] = rand_bf16(rng, (I, H), 0.02)
+        w[p + "mlp.down_proj.weight"] = rand_bf16(rng, (H, I), 0.02)
+    w["model.norm.weight"] = rand_bf16(rng, H, 0.1, 1.0)
+    return w

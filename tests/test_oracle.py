@@ -1,7 +1,9 @@
 """Pins the CPU oracle (oracle/oracle.c) with checks that do not restate its formulas: libm,
 exact decimal arithmetic, closed forms, invariants, brute force, and the reference's published
 byte counts. Each test names the oracle function and the plausible mistake it would catch."""
+import json
 import math
+import os
 from decimal import Decimal, getcontext
 
 import numpy as np
@@ -367,3 +369,56 @@ def test_byte_counts_match_published(oracle):
         wb = oracle.lib().orc_weight_bytes_per_step(ctypes.byref(m))
         kb = oracle.lib().orc_kv_bytes_per_position(ctypes.byref(m))
         assert wb + kb * (5 + 257 / 2) == total, name
+
+
+# ---------------------------------------------------------------- HF golden fixture
+
+HF_FIXTURE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "hf_small_qwen3.npz")
+LOGIT_TOL = 2e-2  # the north star's final-logits bound against the HF path
+TIE_GAP = 0.25    # ref/compare.py:18: a greedy flip is accepted only below this top-2 gap
+
+
+def hf_fixture():
+    f = np.load(HF_FIXTURE)  # allow_pickle=False (default): plain arrays and a JSON string
+    return f, json.loads(str(f["meta"]))
+
+
+def small_oracle(oracle):
+    from conftest import SMALL, small_weights
+    cfg = dict(SMALL, rms_norm_eps=1e-6, rope_theta=1e6)
+    return oracle.Model(cfg, small_weights(0), max_seq=64)
+
+
+@pytest.mark.parametrize("mode", ["GPU_ORDER", "EXACT"])
+def test_oracle_logits_match_hf_fixture(oracle, mode):
+    """The oracle's whole step against HF transformers' Qwen3 (bf16, eager attention, CPU) on
+    the small seeded model: teacher-forced logits at every position within 2e-2."""
+    f, meta = hf_fixture()
+    m = small_oracle(oracle)
+    worst = 0.0
+    for pos, tok in enumerate(meta["tokens"]):
+        m.forward(tok, pos, getattr(oracle, mode))
+        diff = np.abs(bf16_vals(m.logits).astype(np.float64) - f["logits"][pos])
+        worst = max(worst, float(diff.max()))
+    assert worst <= LOGIT_TOL, worst
+    # and not trivially: the logits are not all near zero
+    assert np.abs(f["logits"]).max() > 10 * LOGIT_TOL
+
+
+def test_oracle_greedy_matches_hf_fixture(oracle):
+    """Greedy tokens after the fixture's prompt equal HF's, or part from them only at a near tie
+    (HF's top-2 gap at that step <= TIE_GAP, the reference's greedy rule, ref/greedy.py:14-31)."""
+    f, meta = hf_fixture()
+    m = small_oracle(oracle)
+    prompt = meta["prompt"]
+    for pos, tok in enumerate(prompt):
+        t = m.forward(tok, pos, oracle.GPU_ORDER)
+    got = [t]
+    for i in range(len(f["greedy"]) - 1):
+        t = m.forward(t, len(prompt) + i, oracle.GPU_ORDER)
+        got.append(t)
+    ref = [int(x) for x in f["greedy"]]
+    for i, (a, b) in enumerate(zip(got, ref)):
+        if a != b:
+            assert f["greedy_gap"][i] <= TIE_GAP, (i, a, b, float(f["greedy_gap"][i]))
+            break

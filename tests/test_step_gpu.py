@@ -11,7 +11,7 @@ import struct
 import numpy as np
 import pytest
 
-from conftest import bf16_bits, bf16_vals, rand_bf16
+from conftest import SMALL, bf16_bits, bf16_vals, rand_bf16, small_weights
 
 pytestmark = pytest.mark.gpu
 
@@ -34,33 +34,6 @@ def write_safetensors(path, tensors):
     h = json.dumps(header).encode()
     h += b" " * ((-len(h)) % 16)
     path.write_bytes(struct.pack("<Q", len(h)) + h + b"".join(blobs))
-
-
-SMALL = dict(hidden_size=256, intermediate_size=512, n_layers=2, n_heads=4, n_kv_heads=2,
-             head_dim=128, vocab_size=1000)
-
-
-def small_weights(seed=0):
-    rng = np.random.default_rng(seed)
-    c = SMALL
-    H, I, D = c["hidden_size"], c["intermediate_size"], c["head_dim"]
-    qd, kvd = c["n_heads"] * D, c["n_kv_heads"] * D
-    w = {"model.embed_tokens.weight": rand_bf16(rng, (c["vocab_size"], H), 0.02)}
-    for l in range(c["n_layers"]):
-        p = f"model.layers.{l}."
-        w[p + "input_layernorm.weight"] = rand_bf16(rng, H, 0.1, 1.0)
-        w[p + "self_attn.q_proj.weight"] = rand_bf16(rng, (qd, H), 0.02)
-        w[p + "self_attn.k_proj.weight"] = rand_bf16(rng, (kvd, H), 0.02)
-        w[p + "self_attn.v_proj.weight"] = rand_bf16(rng, (kvd, H), 0.02)
-        w[p + "self_attn.q_norm.weight"] = rand_bf16(rng, D, 0.1, 1.0)
-        w[p + "self_attn.k_norm.weight"] = rand_bf16(rng, D, 0.1, 1.0)
-        w[p + "self_attn.o_proj.weight"] = rand_bf16(rng, (H, qd), 0.02)
-        w[p + "post_attention_layernorm.weight"] = rand_bf16(rng, H, 0.1, 1.0)
-        w[p + "mlp.gate_proj.weight"] = rand_bf16(rng, (I, H), 0.02)
-        w[p + "mlp.up_proj.weight"] = rand_bf16(rng, (I, H), 0.02)
-        w[p + "mlp.down_proj.weight"] = rand_bf16(rng, (H, I), 0.02)
-    w["model.norm.weight"] = rand_bf16(rng, H, 0.1, 1.0)
-    return w
 
 
 def oracle_cfg(c):
@@ -169,6 +142,35 @@ def test_generate_greedy_matches_step_loop(small_model, oracle):
         t = orc.forward(t, len(prompt) + i)
         ref.append(t)
     assert loop == ref
+
+
+def test_small_model_matches_hf_fixture(small_model):
+    """The GPU step (loaded through the safetensors loader) against HF transformers' Qwen3 on the
+    same weights (tests/golden/hf_small_qwen3.npz: bf16, eager attention, CPU): teacher-forced
+    logits within 2e-2 at every position, and the greedy tokens after the fixture's prompt equal
+    to HF's up to a near tie (top-2 gap <= TIE_GAP where they part)."""
+    import json
+    import os
+    ident("small model vs HF fixture")
+    dec, _ = small_model
+    f = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                             "hf_small_qwen3.npz"))
+    meta = json.loads(str(f["meta"]))
+    dec.capture_graph()
+    for pos, tok in enumerate(meta["tokens"]):
+        dec.forward(tok, pos)
+        dec.sample_argmax()
+        diff = np.abs(bf16_vals(dec.logits()).astype(np.float64) - f["logits"][pos])
+        assert diff.max() <= 2e-2, (pos, float(diff.max()))
+    prompt = meta["prompt"]
+    for pos, tok in enumerate(prompt):
+        dec.forward(tok, pos)
+    first = dec.sample_argmax()
+    got = [first] + dec.generate_greedy(first, len(prompt), len(f["greedy"]) - 1)
+    for i, (a, b) in enumerate(zip(got, [int(x) for x in f["greedy"]])):
+        if a != b:
+            assert f["greedy_gap"][i] <= TIE_GAP, (i, a, b, float(f["greedy_gap"][i]))
+            break
 
 
 @pytest.fixture(scope="module")
