@@ -262,6 +262,20 @@ class Decoder:
         copy_to_host(ptr, numel * 2, out)
         return out
 
+    def set_weights(self, weights):
+        """Overwrites device weight tensors with host arrays {safetensors name: uint16 bf16 bits}
+        (every name must exist, with the tensor's element count)."""
+        import numpy as np
+        t = self.tensors()
+        for name, arr in weights.items():
+            if name not in t:
+                raise LlmError(f"no weight tensor {name}")
+            ptr, numel = t[name]
+            a = np.ascontiguousarray(arr, dtype=np.uint16).reshape(-1)
+            if a.size != numel:
+                raise LlmError(f"{name}: {a.size} elements for a tensor of {numel}")
+            copy_to_device(ptr, a)
+
     def host_weights(self):
         """{safetensors name: uint16 numpy array} of every weight (2-D for matrices)."""
         c = self.cfg

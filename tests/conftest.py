@@ -104,15 +104,17 @@ def within_one_ulp_then_scale(y, n_exact, scale):
     return ok
 
 
-# The small Qwen3 of the end-to-end tests and of the HF golden fixture (tests/golden): seeded
-# N(0, 0.02) matrices and 1 + N(0, 0.1) norm weights, as bf16 bits, in the checkpoint's names.
+# Seeded Qwen3 weights as bf16 bits in the checkpoint's names: N(0, 0.02) matrices and
+# 1 + N(0, 0.1) norm weights, drawn in this fixed order from numpy's default_rng(seed), so the HF
+# golden fixtures (tests/golden) and the GPU tests build the same model.
 SMALL = dict(hidden_size=256, intermediate_size=512, n_layers=2, n_heads=4, n_kv_heads=2,
              head_dim=128, vocab_size=1000)
+QWEN3_06B = dict(hidden_size=1024, intermediate_size=3072, n_layers=28, n_heads=16, n_kv_heads=8,
+                 head_dim=128, vocab_size=151936)
 
 
-def small_weights(seed=0):
+def qwen3_np_weights(c, seed=0):
     rng = np.random.default_rng(seed)
-    c = SMALL
     H, I, D = c["hidden_size"], c["intermediate_size"], c["head_dim"]
     qd, kvd = c["n_heads"] * D, c["n_kv_heads"] * D
     w = {"model.embed_tokens.weight": rand_bf16(rng, (c["vocab_size"], H), 0.02)}
@@ -131,3 +133,7 @@ def small_weights(seed=0):
         w[p + "mlp.down_proj.weight"] = rand_bf16(rng, (H, I), 0.02)
     w["model.norm.weight"] = rand_bf16(rng, H, 0.1, 1.0)
     return w
+
+
+def small_weights(seed=0):
+    return qwen3_np_weights(SMALL, seed)

@@ -1,17 +1,20 @@
-"""Writes tests/golden/hf_small_qwen3.npz: the HF-transformers Qwen3 path (the reference's parity
-path, ref/dump.py:124: bf16 weights, eager attention, on the CPU) run on the small seeded model of
-tests/conftest.py (SMALL, small_weights(0)).
+"""Writes the HF golden fixtures: the HF-transformers Qwen3 path (the reference's parity path,
+ref/dump.py:124: bf16 weights, eager attention), run on the CPU in this container, on models whose
+weights come from tests/conftest.py's seeded generator.
 
-Recorded, for the token sequence TOKENS:
+tests/golden/hf_small_qwen3.npz, the small model (SMALL, small_weights(0)), token sequence TOKENS:
   logits      [len(TOKENS), vocab] fp32: teacher-forced logits at every position (one forward)
   greedy      [GREEDY_STEPS] int32: greedy tokens after PROMPT (model.generate, no sampling)
   greedy_gap  [GREEDY_STEPS] fp32: top-1 minus top-2 logit at each greedy step
+tests/golden/hf_qwen3_06b_greedy.npz, the Qwen3-0.6B shapes (QWEN3_06B, qwen3_np_weights(., 0)),
+the bench's 5 seeded prompt ids:
+  greedy, greedy_gap  [256]; top_values, top_indices [256, 8]: the 8 largest logits per step
 
 These pin what no closed form does: the HF fp32/bf16 CPU arithmetic end to end (the e2e logits
-within 2e-2 and the greedy sequence up to near ties). The fixture is data; this script is the
+within 2e-2 and the greedy sequence up to near ties). The fixtures are data; this script is the
 only place transformers is imported, and only here (never on the GPU box).
 
-Run from the repository root:  python tests/golden/make_hf_fixtures.py
+Run from the repository root:  python tests/golden/make_hf_fixtures.py [small] [0.6B]
 """
 import json
 import os
@@ -25,26 +28,25 @@ sys.path.insert(0, os.path.dirname(HERE))  # tests/ (conftest helpers)
 TOKENS = [17, 999, 0, 512, 3, 77, 640, 1, 2, 900, 45, 300]
 PROMPT = [5, 60, 700, 8, 91]
 GREEDY_STEPS = 40
+# The Qwen3-0.6B-shaped model (28 layers) of the bench's decode: 5 seeded prompt ids, 256 greedy
+# tokens; per step the top-2 gap and the 8 largest logits (values, indices).
+GREEDY_06B_STEPS = 256
+TOPK = 8
 
 
-def main():
+def hf_model(c, w, max_pos=64):
+    """transformers' Qwen3ForCausalLM (bf16, eager attention) with the given bf16-bit weights."""
     import torch
-    import transformers
     from transformers import Qwen3Config, Qwen3ForCausalLM
-
-    from conftest import SMALL, small_weights
-
-    c = SMALL
     cfg = Qwen3Config(
         vocab_size=c["vocab_size"], hidden_size=c["hidden_size"],
         intermediate_size=c["intermediate_size"], num_hidden_layers=c["n_layers"],
         num_attention_heads=c["n_heads"], num_key_value_heads=c["n_kv_heads"],
-        head_dim=c["head_dim"], max_position_embeddings=64, rms_norm_eps=1e-6,
+        head_dim=c["head_dim"], max_position_embeddings=max_pos, rms_norm_eps=1e-6,
         rope_parameters={"rope_type": "default", "rope_theta": 1e6}, tie_word_embeddings=True,
         attention_bias=False, hidden_act="silu", attn_implementation="eager")
     torch.manual_seed(0)
     model = Qwen3ForCausalLM(cfg).to(torch.bfloat16).eval()
-    w = small_weights(0)
     state = {}
     for name, bits in w.items():
         t = torch.from_numpy(np.ascontiguousarray(bits, dtype=np.uint16).view(np.int16))
@@ -56,7 +58,17 @@ def main():
     assert model.lm_head.weight.data_ptr() == model.model.embed_tokens.weight.data_ptr() or \
         torch.equal(model.lm_head.weight, model.model.embed_tokens.weight)
     assert model.config._attn_implementation == "eager"
+    return model
 
+
+def small_fixture():
+    import torch
+    import transformers
+
+    from conftest import SMALL, small_weights
+
+    c = SMALL
+    model = hf_model(c, small_weights(0))
     with torch.no_grad():
         ids = torch.tensor([TOKENS])
         logits = model(ids).logits[0].float().numpy()
@@ -78,5 +90,39 @@ def main():
     print("wrote hf_small_qwen3.npz:", logits.shape, greedy[:8], "min gap", min(gaps))
 
 
+def qwen06b_fixture():
+    import torch
+    import transformers
+
+    from conftest import QWEN3_06B, qwen3_np_weights
+
+    c = QWEN3_06B
+    model = hf_model(c, qwen3_np_weights(c, 0), max_pos=4096)
+    prompt = [int(t) for t in np.random.default_rng(0).integers(0, c["vocab_size"], 5)]
+    with torch.no_grad():
+        out = model.generate(torch.tensor([prompt]), max_new_tokens=GREEDY_06B_STEPS,
+                             do_sample=False, output_logits=True, return_dict_in_generate=True,
+                             pad_token_id=0, eos_token_id=None)
+    greedy = out.sequences[0, len(prompt):].numpy().astype(np.int32)
+    gaps, top_v, top_i = [], [], []
+    for step_logits in out.logits:
+        top = torch.topk(step_logits[0].float(), TOPK)
+        gaps.append(float(top.values[0] - top.values[1]))
+        top_v.append(top.values.numpy())
+        top_i.append(top.indices.numpy().astype(np.int32))
+    meta = {"transformers": transformers.__version__, "torch": torch.__version__,
+            "dtype": "bfloat16", "attn_implementation": "eager", "device": "cpu",
+            "model": dict(c), "weights": "tests/conftest.py qwen3_np_weights(QWEN3_06B, 0)",
+            "prompt": prompt}
+    np.savez_compressed(os.path.join(HERE, "hf_qwen3_06b_greedy.npz"), greedy=greedy,
+                        greedy_gap=np.array(gaps, np.float32), top_values=np.array(top_v),
+                        top_indices=np.array(top_i), meta=np.array(json.dumps(meta)))
+    print("wrote hf_qwen3_06b_greedy.npz:", greedy[:8], "min gap", min(gaps))
+
+
 if __name__ == "__main__":
-    main()
+    which = sys.argv[1:] or ["small", "0.6B"]
+    if "small" in which:
+        small_fixture()
+    if "0.6B" in which:
+        qwen06b_fixture()
