@@ -143,6 +143,9 @@ void free_run_state(RunState *s);
 void capture_graph(const Config *cfg, const Weights *w, RunState *s);
 void forward(const Config *cfg, const Weights *w, RunState *s, int token, int pos);
 int sample_argmax(const Config *cfg, RunState *s);
+/* src/forward.cuh:32. A token drawn from softmax(logits / temperature) at the coin in [0, 1)
+ * (sample_forward); an error if the draw finds none. */
+int sample_temperature(const Config *cfg, RunState *s, float temperature, float coin);
 size_t weight_bytes_per_step(const Config *cfg);
 size_t kv_bytes_per_position(const Config *cfg);
 

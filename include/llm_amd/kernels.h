@@ -74,6 +74,12 @@ void attention_forward(bf16 *out, const bf16 *q, const bf16 *key_cache, const bf
  * results live in one library-owned device buffer. */
 void argmax_forward(int *out, const bf16 *x, int n, hipStream_t stream);
 
+/* src/kernels.cuh:26. *out = a token drawn from softmax(x * inv_temp) by inverse CDF at the
+ * coin u in [0, 1): the row's max, 1024 contiguous chunks whose weights exp((x - max) * inv_temp)
+ * are added in order, the chunk sums added in order, then the first chunk and element whose
+ * running sum passes u * total (-1 if none). */
+void sample_forward(int *out, const bf16 *x, int n, float inv_temp, float u, hipStream_t stream);
+
 /* ---- entry points with no counterpart in kernels.cuh (needed by the multi-row workloads) ---- */
 
 /* qk_norm_rope_forward over n_tokens rows: q [n_tokens, n_heads*D], k and v

@@ -21,7 +21,7 @@ __all__ = [
     "gemv_residual_forward", "qkv_forward", "gate_up_forward", "qk_norm_rope_forward",
     "qk_norm_rope_rows", "attention_forward", "argmax_forward", "swiglu_forward",
     "attention_workspace_floats", "rmsnorm_qkv_forward", "rmsnorm_gemv_forward",
-    "rmsnorm_gate_up_forward", "hbm_stream_probe", "EXPORTED_SYMBOLS",
+    "rmsnorm_gate_up_forward", "hbm_stream_probe", "sample_forward", "EXPORTED_SYMBOLS",
 ]
 
 # Every symbol include/llm_amd/*.h declares.
@@ -30,7 +30,7 @@ EXPORTED_SYMBOLS = [
     "qkv_forward", "gate_up_forward", "qk_norm_rope_forward", "attention_forward",
     "argmax_forward", "qk_norm_rope_rows", "swiglu_forward", "attention_workspace_floats",
     "rmsnorm_qkv_forward", "rmsnorm_gemv_forward", "rmsnorm_gate_up_forward",
-    "hbm_stream_probe", "llm_set_exit_on_error", "llm_last_error", "llm_clear_error",
+    "hbm_stream_probe", "sample_forward", "sample_temperature", "llm_set_exit_on_error", "llm_last_error", "llm_clear_error",
     "load_config", "load_weights", "free_weights", "print_weight_checksums",
     "alloc_run_state", "free_run_state", "capture_graph", "forward", "sample_argmax",
     "weight_bytes_per_step", "kv_bytes_per_position", "alloc_run_state_seq", "synth_weights",
@@ -66,6 +66,7 @@ _SIGS = {
     "rmsnorm_gemv_forward": (None, [_vp] * 4 + [_f, _i, _i, _vp]),
     "rmsnorm_gate_up_forward": (None, [_vp] * 5 + [_f, _i, _i, _vp]),
     "hbm_stream_probe": (None, [_vp, _vp, _vp, _sz, _i, _vp]),
+    "sample_forward": (None, [_vp, _vp, _i, _f, _f, _vp]),
     "llm_set_exit_on_error": (_i, [_i]),
     "llm_last_error": (ctypes.c_char_p, []),
     "llm_clear_error": (None, []),
@@ -225,6 +226,10 @@ def hbm_stream_probe(dst, a, b, n_bytes, mode, stream=None):
     if not isinstance(dst, int) and dst.numel() * dst.element_size() < need:
         raise LlmError(f"dst holds {dst.numel() * dst.element_size()} bytes, the probe needs {need}")
     _call(lib().hbm_stream_probe, _ptr(dst), _ptr(a), _ptr(b), n_bytes, mode, _stream(stream))
+
+
+def sample_forward(out, x, n, inv_temp, u, stream=None):
+    _call(lib().sample_forward, _ptr(out), _bf16(x, "x"), n, inv_temp, u, _stream(stream))
 
 
 def argmax_forward(out, x, n, stream=None):

@@ -321,6 +321,24 @@ extern "C" void forward(const Config *cfg, const Weights *w, RunState *s, int to
 }
 
 // src/forward.cu:229-236
+// src/forward.cu:238-251: a token drawn from softmax(logits / temperature) at the coin; the
+// argmax a persistent step left in next_token is overwritten.
+extern "C" int sample_temperature(const Config *cfg, RunState *s, float temperature, float coin) {
+    const float inv_temp = 1.0f / temperature;
+    sample_forward(s->next_token, s->logits, cfg->vocab_size, inv_temp, coin, s->stream);
+    s->next_token_valid = 0;
+    int token = -1;
+    if (!HIP_OK(hipMemcpyAsync(&token, s->next_token, 4, hipMemcpyDeviceToHost, s->stream)))
+        return -1;
+    if (!HIP_OK(hipStreamSynchronize(s->stream))) return -1;
+    if (s->persistent && !check_step_error(cfg, s)) return -1;
+    if (token < 0) {
+        llm_fail("sampling found no token (coin %g)", (double)coin);
+        return -1;
+    }
+    return token;
+}
+
 extern "C" int sample_argmax(const Config *cfg, RunState *s) {
     if (!s->next_token_valid) argmax_into_next(cfg, s);  // the persistent step already did it
     int token = -1;

@@ -1219,6 +1219,65 @@ extern "C" void attention_forward(bf16 *out, const bf16 *q, const bf16 *key_cach
 }
 
 // ------------------------------------------------------------------------------------------
+// temperature sampling (src/kernels.cu:546-597)
+// ------------------------------------------------------------------------------------------
+
+// Inverse-CDF sampling from softmax(x * inv_temp), one workgroup of SAMPLE_T threads. The
+// additions keep the reference's order, so the chosen index follows from the weights alone: the
+// row's max; thread t adds the weights exp((x - max) * inv_temp) of the contiguous chunk
+// [t c, t c + c) in order (c = ceil(n / SAMPLE_T)); thread 0 adds the chunk sums in order for the
+// total, walks them to the chunk holding u * total (never past the last) and then that chunk's
+// elements to the first whose running sum passes it (-1 if none does). Not on the decode path.
+constexpr int SAMPLE_T = 1024;
+
+__global__ __launch_bounds__(SAMPLE_T) void sample_kernel(int *out, const bf16 *x, int n,
+                                                          float inv_temp, float u) {
+    __shared__ float sums[SAMPLE_T];
+    __shared__ float wmax[SAMPLE_T / 64];
+    const int t = threadIdx.x;
+    float m = -__builtin_huge_valf();
+    for (int i = t; i < n; i += SAMPLE_T) m = fmaxf(m, bf2f(x[i]));
+    m = wave_max(m);
+    if ((t & 63) == 0) wmax[t >> 6] = m;
+    __syncthreads();
+    float mx = wmax[0];
+    for (int w = 1; w < SAMPLE_T / 64; w++) mx = fmaxf(mx, wmax[w]);  // max: any order
+    const int chunk = (n + SAMPLE_T - 1) / SAMPLE_T;
+    const int start = t * chunk, end = min(start + chunk, n);
+    float acc = 0.0f;
+    for (int i = start; i < end; i++) acc += exp_f32((bf2f(x[i]) - mx) * inv_temp);
+    sums[t] = acc;
+    __syncthreads();
+    if (t != 0) return;
+    float total = 0.0f;
+    for (int k = 0; k < SAMPLE_T; k++) total += sums[k];
+    const float target = u * total;
+    float cdf = 0.0f;
+    int k = 0;
+    while (k < SAMPLE_T - 1 && cdf + sums[k] <= target) cdf += sums[k++];
+    int chosen = -1;
+    float run = 0.0f;
+    for (int i = k * chunk; i < min(k * chunk + chunk, n); i++) {
+        run += exp_f32((bf2f(x[i]) - mx) * inv_temp);
+        if (cdf + run > target) {
+            chosen = i;
+            break;
+        }
+    }
+    *out = chosen;
+}
+
+extern "C" void sample_forward(int *out, const bf16 *x, int n, float inv_temp, float u,
+                               hipStream_t stream) {
+    if (n <= 0) {
+        llm_fail("sample: n %d must be positive", n);
+        return;
+    }
+    sample_kernel<<<1, SAMPLE_T, 0, stream>>>(out, x, n, inv_temp, u);
+    LAUNCH_OK();
+}
+
+// ------------------------------------------------------------------------------------------
 // streaming ceiling probe (measurement helper)
 // ------------------------------------------------------------------------------------------
 

@@ -70,6 +70,7 @@ _SIGS = {
     "capture_graph": (None, [_PC, _PW, _PS]),
     "forward": (None, [_PC, _PW, _PS, _i, _i]),
     "sample_argmax": (_i, [_PC, _PS]),
+    "sample_temperature": (_i, [_PC, _PS, _f, _f]),
     "weight_bytes_per_step": (_sz, [_PC]),
     "kv_bytes_per_position": (_sz, [_PC]),
     "synth_weights": (None, [_PC, _PW, ctypes.c_uint64, _f, _f]),
@@ -237,6 +238,14 @@ class Decoder:
 
     def sample_argmax(self):
         t = lib().sample_argmax(ctypes.byref(self.cfg), ctypes.byref(self.s))
+        check()
+        return t
+
+    def sample_temperature(self, temperature, coin):
+        """A token drawn from softmax(logits / temperature) at coin in [0, 1)
+        (src/forward.cu:238-251)."""
+        t = lib().sample_temperature(ctypes.byref(self.cfg), ctypes.byref(self.s), temperature,
+                                     coin)
         check()
         return t
 

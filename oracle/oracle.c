@@ -14,26 +14,32 @@
  *   orc_qk_norm_rope   src/kernels.cu:301-384, HF modeling_qwen3.py:121,:126-170,:252-253
  *   orc_attention      src/kernels.cu:439-486, HF modeling_qwen3.py:185-207 (eager attention)
  *   orc_argmax         src/kernels.cu:499-538
+ *   orc_sample         src/kernels.cu:546-597 (inverse-CDF temperature sampling)
  *   orc_forward        src/forward.cu:118-193 (layer order), :229-236 (greedy sample)
  *   orc_*_bytes        src/forward.cu:83-114
  *
- * Parity pinning (tests/test_oracle.py, tests/test_golden.py):
- *   bf16 rounding      exhaustive check against numpy round-half-even over all fp32 classes,
- *                      and against torch's fp32->bf16 cast (golden vectors).
+ * Parity pinning (tests/test_oracle.py; no check restates the formula it pins):
+ *   bf16 rounding      an independent nearest/ties-to-even selection over 215k patterns
+ *                      (exact ties, overflow, denormals, NaN).
  *   orc_exp_f32        every fp32 input in [-104, 89] against (float)exp((double)x): <= 1 ulp.
- *   orc_sincos_d       540k RoPE angles against libm cos/sin: identical after fp32 rounding.
- *   orc_inv_freq       against exact decimal pow (correct rounding) and torch's table.
- *   orc_rmsnorm        closed forms (zero row, constant row, gamma=1, scale invariance) and HF
- *                      Qwen3RMSNorm golden vectors (<= 1 bf16 ulp).
- *   orc_dot/gemv       double brute force (<= 1 bf16 ulp + fp32 reduction bound), GPU-order vs
- *                      exact, HF nn.Linear golden vectors.
- *   orc_swiglu/gate_up closed forms (g=0, large +-g) and HF Qwen3MLP golden vectors.
- *   orc_qk_norm_rope   pos=0 identity, frequency-1 pair angle = pos, norm preservation, HF
- *                      q_norm/k_norm + apply_rotary_pos_emb golden vectors; KV slot invariants.
- *   orc_attention      single position (output = v), uniform scores (mean of v), HF eager
- *                      attention golden vectors.
+ *   orc_sincos_d       libm cos/sin at every RoPE angle of two (theta, D) tables: identical
+ *                      after fp32 rounding.
+ *   orc_inv_freq       60-digit decimal pow: correctly rounded.
+ *   orc_rmsnorm        closed forms (zero row, constant row, power-of-two scale invariance) and
+ *                      a double-precision reference (<= 1 bf16 ulp at HF's rounding point).
+ *   orc_dot/gemv       double brute force (<= 1 bf16 ulp + the fp32 accumulation bound).
+ *   orc_gemv_residual  the tap equals the GEMV, the add equals bf16(x + tap) (ref/dump.py:104-108).
+ *   orc_swiglu/gate_up closed forms (g = 0, large +-g), every finite bf16 gate against libm
+ *                      double silu (1 ulp), gate_up = gemv + swiglu.
+ *   orc_qk_norm_rope   pos 0 is the identity, the frequency-1 pair rotates by pos exactly,
+ *                      norm preservation, KV slot invariants against a sentinel fill.
+ *   orc_attention      single position (output = v), equal keys (mean of v), a double softmax
+ *                      reference within 2 ulps.
  *   orc_argmax         brute force, ties, -inf, last index, NaN policy.
- *   orc_forward        HF Qwen3ForCausalLM golden logits and greedy tokens (small model).
+ *   orc_sample         u -> 0 and u -> 1 pick the first and last tokens with weight, a one-hot
+ *                      row picks its token for every u, uniform rows pick floor(u n).
+ *   orc_forward        HF transformers' Qwen3ForCausalLM on the small seeded model
+ *                      (tests/golden/hf_small_qwen3.npz): logits within 2e-2, greedy tokens.
  *   byte formulas      the reference's published bytes/step (bench/results.csv:289,:317,:345).
  */
 #include "oracle.h"
@@ -569,6 +575,38 @@ int orc_argmax(const uint16_t *x, int n) {
         }
     }
     return idx;
+}
+
+/* Inverse-CDF sampling from softmax(x * inv_temp) (src/kernels.cu:546-597): the row's max; the
+ * row cut into 1024 contiguous chunks of ceil(n / 1024) elements, each chunk's weights
+ * exp_f32((x - max) * inv_temp) added in order; the total as the chunk sums added in order;
+ * target = u * total; the first chunk whose running sum would pass the target (never past the
+ * last), then the first element of it whose running sum passes. -1 if none does. */
+int orc_sample(const uint16_t *x, int n, float inv_temp, float u) {
+    enum { T = 1024 };
+    float mx = -INFINITY;
+    for (int i = 0; i < n; i++) mx = fmaxf(mx, bf(x[i]));
+    const int chunk = (n + T - 1) / T;
+    float sums[T];
+    for (int t = 0; t < T; t++) {
+        const int start = t * chunk, end = start + chunk < n ? start + chunk : n;
+        float acc = 0.0f;
+        for (int i = start; i < end; i++) acc += orc_exp_f32((bf(x[i]) - mx) * inv_temp);
+        sums[t] = acc;
+    }
+    float total = 0.0f;
+    for (int t = 0; t < T; t++) total += sums[t];
+    const float target = u * total;
+    float cdf = 0.0f;
+    int t = 0;
+    while (t < T - 1 && cdf + sums[t] <= target) cdf += sums[t++];
+    const int start = t * chunk, end = start + chunk < n ? start + chunk : n;
+    float acc = 0.0f;
+    for (int i = start; i < end; i++) {
+        acc += orc_exp_f32((bf(x[i]) - mx) * inv_temp);
+        if (cdf + acc > target) return i;
+    }
+    return -1;
 }
 
 /* ------------------------------------------------------------------------------------------ */

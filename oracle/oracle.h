@@ -70,6 +70,7 @@ void orc_attention(uint16_t *out, const uint16_t *q, const uint16_t *key_cache,
                    const uint16_t *value_cache, int n_heads, int n_kv_heads, int head_dim, int pos,
                    float scale, int mode);
 int orc_argmax(const uint16_t *x, int n);
+int orc_sample(const uint16_t *x, int n, float inv_temp, float u);
 
 /* ---- whole decode step (src/forward.cu:118-193, :229-236) ---- */
 typedef struct {

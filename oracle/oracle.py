@@ -87,6 +87,7 @@ def _declare(L):
                                   [_c_float, _c_float, _u16p, _u16p, _c_int]),
         "orc_attention": (None, [_u16p] * 4 + [_c_int] * 4 + [_c_float, _c_int]),
         "orc_argmax": (_c_int, [_u16p, _c_int]),
+        "orc_sample": (_c_int, [_u16p, _c_int, ctypes.c_float, ctypes.c_float]),
         "orc_forward": (_c_int, [ctypes.POINTER(OrcConfig), ctypes.POINTER(OrcWeights),
                                  ctypes.POINTER(OrcState), _c_int, _c_int, _c_int]),
         "orc_weight_bytes_per_step": (_c_size, [ctypes.POINTER(OrcConfig)]),
@@ -223,6 +224,11 @@ def attention(q, key_cache, value_cache, n_heads, n_kv_heads, head_dim, pos, sca
 
 def argmax(x):
     return lib().orc_argmax(_p(np.ascontiguousarray(x, dtype=np.uint16)), x.size)
+
+
+def sample(x, inv_temp, u):
+    x = np.ascontiguousarray(x, dtype=np.uint16)
+    return lib().orc_sample(_p(x), x.size, inv_temp, u)
 
 
 def selfcheck_exp(lo, hi):

@@ -352,6 +352,29 @@ def test_hbm_stream_probe(gpu):
     assert np.array_equal(out.cpu().numpy().astype(np.uint32), expect)
 
 
+# ---------------------------------------------------------------- temperature sampling
+
+def test_sample_forward(gpu, oracle):
+    """sample_forward equals the oracle's inverse-CDF draw (same weights, same order of additions)
+    on random rows, one-hot rows and uniform rows, for several temperatures and coins."""
+    import torch
+    ident("sample_forward")
+    rng = np.random.default_rng(11)
+    out = torch.zeros(1, dtype=torch.int32, device="cuda")
+    n = 151936
+    rows = [rand_bf16(rng, n, s) for s in (0.5, 2.0, 4.0)]
+    hot = bf16_bits(np.full(n, -50.0, np.float32))
+    hot[123456] = bf16_bits(np.array([50.0], np.float32))[0]
+    rows += [hot, bf16_bits(np.zeros(n, np.float32)), rand_bf16(rng, 1000, 1.0),
+             rand_bf16(rng, 1023, 1.0)]
+    for row in rows:
+        xd = dev(row)
+        for inv_temp in (1.0, 0.7, 1.5):
+            for u in (0.0, 0.25, 0.5, 0.9, 0.999):
+                gpu.sample_forward(out, xd, row.size, inv_temp, u)
+                assert int(out.item()) == oracle.sample(row, inv_temp, u), (row.size, inv_temp, u)
+
+
 # ---------------------------------------------------------------- argmax
 
 def test_argmax(gpu, oracle):

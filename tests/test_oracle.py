@@ -422,3 +422,40 @@ def test_oracle_greedy_matches_hf_fixture(oracle):
         if a != b:
             assert f["greedy_gap"][i] <= TIE_GAP, (i, a, b, float(f["greedy_gap"][i]))
             break
+
+
+# ---------------------------------------------------------------- temperature sampling
+
+def test_sample_closed_forms(oracle):
+    """orc_sample (src/kernels.cu:546-597): a uniform row gives floor(u n); a one-hot row gives
+    its token for every u; u = 0 gives the first token with weight. Catches an off-by-one in the
+    chunk walk or an inverted comparison."""
+    n = 151936
+    flat = bf16_bits(np.zeros(n, np.float32))
+    for u in [0.0, 0.1, 0.37, 0.5, 0.999]:
+        assert oracle.sample(flat, 1.0, u) == int(u * n), u
+    hot = bf16_bits(np.full(n, -100.0, np.float32))
+    for k in [0, 7, 77777, n - 1]:
+        h = hot.copy()
+        h[k] = bf16_bits(np.array([100.0], np.float32))[0]
+        for u in [0.0, 0.5, 0.999999]:
+            assert oracle.sample(h, 1.0, u) == k, (k, u)
+    row = rand_bf16(np.random.default_rng(3), n, 2.0)
+    assert oracle.sample(row, 1.0, 0.0) == 0
+
+
+def test_sample_against_double_cdf(oracle):
+    """Random rows: the chosen index brackets u in the float64 CDF of the same weights (up to the
+    fp32 accumulation error), and a higher temperature spreads the draws."""
+    rng = np.random.default_rng(5)
+    n = 20000
+    for trial in range(6):
+        row = rand_bf16(rng, n, 3.0)
+        inv_temp = [1.0, 0.5, 2.0][trial % 3]
+        x = bf16_vals(row).astype(np.float64)
+        w = np.exp((x - x.max()) * inv_temp)
+        cdf = np.cumsum(w) / w.sum()
+        for u in rng.random(8):
+            i = oracle.sample(row, inv_temp, float(u))
+            lo = cdf[i - 1] if i > 0 else 0.0
+            assert lo - 1e-5 <= u <= cdf[i] + 1e-5, (trial, u, i, lo, cdf[i])

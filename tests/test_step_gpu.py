@@ -144,6 +144,19 @@ def test_generate_greedy_matches_step_loop(small_model, oracle):
     assert loop == ref
 
 
+def test_sample_temperature_step(small_model, oracle):
+    """sample_temperature after a step draws from the step's logits as the oracle does
+    (src/forward.cu:238-251), with the same coin; coin 0 gives the first token with weight."""
+    ident("sample_temperature")
+    dec, _ = small_model
+    dec.capture_graph()
+    for pos, tok in enumerate([4, 8, 15, 16]):
+        dec.forward(tok, pos)
+    lg = dec.logits()
+    for temp, coin in [(1.0, 0.3), (0.5, 0.77), (2.0, 0.05), (1.0, 0.0)]:
+        assert dec.sample_temperature(temp, coin) == oracle.sample(lg, np.float32(1.0 / temp), coin)
+
+
 def test_small_model_matches_hf_fixture(small_model):
     """The GPU step (loaded through the safetensors loader) against HF transformers' Qwen3 on the
     same weights (tests/golden/hf_small_qwen3.npz: bf16, eager attention, CPU): teacher-forced
