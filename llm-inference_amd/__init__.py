@@ -21,7 +21,8 @@ __all__ = [
     "gemv_residual_forward", "qkv_forward", "gate_up_forward", "qk_norm_rope_forward",
     "qk_norm_rope_rows", "attention_forward", "argmax_forward", "swiglu_forward",
     "attention_workspace_floats", "rmsnorm_qkv_forward", "rmsnorm_gemv_forward",
-    "rmsnorm_gate_up_forward", "hbm_stream_probe", "sample_forward", "EXPORTED_SYMBOLS",
+    "rmsnorm_gate_up_forward", "hbm_stream_probe", "sample_forward", "dump_open",
+    "dump_close", "dump_enabled", "EXPORTED_SYMBOLS",
 ]
 
 # Every symbol include/llm_amd/*.h declares.
@@ -30,7 +31,8 @@ EXPORTED_SYMBOLS = [
     "qkv_forward", "gate_up_forward", "qk_norm_rope_forward", "attention_forward",
     "argmax_forward", "qk_norm_rope_rows", "swiglu_forward", "attention_workspace_floats",
     "rmsnorm_qkv_forward", "rmsnorm_gemv_forward", "rmsnorm_gate_up_forward",
-    "hbm_stream_probe", "sample_forward", "sample_temperature", "llm_set_exit_on_error", "llm_last_error", "llm_clear_error",
+    "hbm_stream_probe", "sample_forward", "sample_temperature", "dump_open", "dump_close",
+    "dump_enabled", "dump_bf16", "dump_f32", "llm_set_exit_on_error", "llm_last_error", "llm_clear_error",
     "load_config", "load_weights", "free_weights", "print_weight_checksums",
     "alloc_run_state", "free_run_state", "capture_graph", "forward", "sample_argmax",
     "weight_bytes_per_step", "kv_bytes_per_position", "alloc_run_state_seq", "synth_weights",
@@ -67,6 +69,11 @@ _SIGS = {
     "rmsnorm_gate_up_forward": (None, [_vp] * 5 + [_f, _i, _i, _vp]),
     "hbm_stream_probe": (None, [_vp, _vp, _vp, _sz, _i, _vp]),
     "sample_forward": (None, [_vp, _vp, _i, _f, _f, _vp]),
+    "dump_open": (None, [ctypes.c_char_p]),
+    "dump_close": (None, []),
+    "dump_enabled": (_i, []),
+    "dump_bf16": (None, [ctypes.c_char_p, _vp, _i]),
+    "dump_f32": (None, [ctypes.c_char_p, _vp, _i]),
     "llm_set_exit_on_error": (_i, [_i]),
     "llm_last_error": (ctypes.c_char_p, []),
     "llm_clear_error": (None, []),
@@ -230,6 +237,15 @@ def hbm_stream_probe(dst, a, b, n_bytes, mode, stream=None):
 
 def sample_forward(out, x, n, inv_temp, u, stream=None):
     _call(lib().sample_forward, _ptr(out), _bf16(x, "x"), n, inv_temp, u, _stream(stream))
+
+
+def dump_open(directory):
+    """Activation dumps of the eager step into `directory` (include/llm_amd/dump.h)."""
+    _call(lib().dump_open, str(directory).encode())
+
+
+def dump_close():
+    lib().dump_close()
 
 
 def argmax_forward(out, x, n, stream=None):

@@ -7,6 +7,7 @@
 
 #include "common.h"
 #include "internal.h"
+#include "llm_amd/dump.h"
 #include "llm_amd/forward.h"
 #include "step.h"
 
@@ -92,16 +93,28 @@ extern "C" size_t kv_bytes_per_position(const Config *cfg) {
 // the step
 // ------------------------------------------------------------------------------------------
 
+// One layer tensor of the dumps: "Lnn.<name>" (src/forward.cu:75-79).
+static void dump_layer(int l, const char *name, const bf16 *d, int n) {
+    char full[64];
+    snprintf(full, sizeof full, "L%02d.%s", l, name);
+    dump_bf16(full, d, n);
+}
+
 static bool forward_kernels(const Config *cfg, const Weights *w, RunState *s) {
     const int H = cfg->hidden_size, D = cfg->head_dim;
     const int q_dim = cfg->n_heads * D, kv_dim = cfg->n_kv_heads * D;
     const int I = cfg->intermediate_size;
     const float scale = (float)(1.0 / sqrt((double)D));
     hipStream_t st = s->stream;
-    // RMSNorm runs as the prologue of the GEMV that reads it (same bits, one launch and one
-    // store/reload of the normed row fewer) for hidden sizes of up to 8192
-    const bool fuse_norm = H <= 8192;
+    // While dumping, every intermediate is kept: the RMSNorms run on their own and the fused
+    // launchers write their taps (src/forward.cu:127-133). Otherwise RMSNorm runs as the prologue
+    // of the GEMV that reads it (same bits, one launch and one store/reload of the normed row
+    // fewer) for hidden sizes of up to 8192.
+    const bool dumping = dump_enabled() != 0;
+    const bool fuse_norm = H <= 8192 && !dumping;
+    bf16 *tap1 = dumping ? s->tap1 : nullptr, *tap2 = dumping ? s->tap2 : nullptr;
     embedding_checked(s->x, w->embed, s->next_token, H, cfg->vocab_size, s->error_flag, st);
+    dump_bf16("embed", s->x, H);
     for (int l = 0; l < cfg->n_layers && !llm_has_error(); l++) {
         const LayerWeights *L = &w->layers[l];
         bf16 *kc = s->key_cache + (size_t)l * s->max_seq * kv_dim;
@@ -111,30 +124,49 @@ static bool forward_kernels(const Config *cfg, const Weights *w, RunState *s) {
                                 cfg->rms_norm_eps, q_dim, kv_dim, H, st);
         } else {
             rmsnorm_forward(s->xb, s->x, L->attn_norm, 1, H, cfg->rms_norm_eps, st);
+            dump_layer(l, "attn_norm", s->xb, H);
             qkv_forward(s->q, s->k, s->v, L->wq, L->wk, L->wv, s->xb, q_dim, kv_dim, H, st);
         }
+        dump_layer(l, "q_proj", s->q, q_dim);
+        dump_layer(l, "k_proj", s->k, kv_dim);
+        dump_layer(l, "v_proj", s->v, kv_dim);
         qk_norm_rope_forward(s->q, s->k, s->v, L->q_norm, L->k_norm, kc, vc, s->pos, cfg->n_heads,
-                             cfg->n_kv_heads, D, cfg->rms_norm_eps, cfg->rope_theta, nullptr,
-                             nullptr, st);
+                             cfg->n_kv_heads, D, cfg->rms_norm_eps, cfg->rope_theta, tap1, tap2,
+                             st);
+        dump_layer(l, "q_norm", tap1, q_dim);
+        dump_layer(l, "k_norm", tap2, kv_dim);
+        dump_layer(l, "q_rope", s->q, q_dim);
+        dump_layer(l, "k_rope", s->k, kv_dim);
         attention_forward(s->attn_out, s->q, kc, vc, s->att, cfg->n_heads, cfg->n_kv_heads, D,
                           s->pos, s->max_seq, scale, st);
-        gemv_residual_forward(s->x, L->wo, s->attn_out, H, q_dim, nullptr, st);
+        dump_layer(l, "attn_out", s->attn_out, q_dim);
+        gemv_residual_forward(s->x, L->wo, s->attn_out, H, q_dim, tap1, st);
+        dump_layer(l, "o_proj", tap1, H);
+        dump_layer(l, "attn_resid", s->x, H);
         if (fuse_norm) {
             rmsnorm_gate_up_forward(s->hb, L->w_gate, L->w_up, s->x, L->mlp_norm,
                                     cfg->rms_norm_eps, I, H, st);
         } else {
             rmsnorm_forward(s->xb, s->x, L->mlp_norm, 1, H, cfg->rms_norm_eps, st);
-            gate_up_forward(s->hb, L->w_gate, L->w_up, s->xb, I, H, nullptr, nullptr, st);
+            dump_layer(l, "mlp_norm", s->xb, H);
+            gate_up_forward(s->hb, L->w_gate, L->w_up, s->xb, I, H, tap1, tap2, st);
         }
-        gemv_residual_forward(s->x, L->w_down, s->hb, H, I, nullptr, st);
+        dump_layer(l, "gate", tap1, I);
+        dump_layer(l, "up", tap2, I);
+        dump_layer(l, "mlp_act", s->hb, I);
+        gemv_residual_forward(s->x, L->w_down, s->hb, H, I, tap1, st);
+        dump_layer(l, "down", tap1, H);
+        dump_layer(l, "out", s->x, H);
     }
     if (fuse_norm) {
         rmsnorm_gemv_forward(s->logits, w->lm_head, s->x, w->final_norm, cfg->rms_norm_eps,
                              cfg->vocab_size, H, st);
     } else {
         rmsnorm_forward(s->xb, s->x, w->final_norm, 1, H, cfg->rms_norm_eps, st);
+        dump_bf16("final_norm", s->xb, H);
         gemv_forward(s->logits, w->lm_head, s->xb, cfg->vocab_size, H, st);
     }
+    dump_bf16("logits", s->logits, cfg->vocab_size);
     return !llm_has_error();
 }
 
@@ -283,6 +315,9 @@ extern "C" void capture_graph(const Config *cfg, const Weights *w, RunState *s) 
         s->graph = nullptr;
     }
     s->persistent = 0;
+    // while dumping, the step runs eagerly (the reference captures only without --dump,
+    // src/main.cu:253): nothing is captured, and forward() dumps as it goes
+    if (dump_enabled()) return;
     const bool want = s->step_mode == STEP_PERSISTENT ||
                       (s->step_mode == STEP_AUTO && step_kernel_preferred(cfg));
     if (want && step_kernel_supported(cfg, s->max_seq)) {
@@ -310,7 +345,9 @@ extern "C" void forward(const Config *cfg, const Weights *w, RunState *s, int to
     set_token_pos_kernel<<<1, 64, 0, s->stream>>>(s->next_token, s->pos, token, pos);
     if (!LAUNCH_OK()) return;
     s->next_token_valid = 0;
-    if (s->persistent) {
+    if (dump_enabled()) {
+        forward_kernels(cfg, w, s);  // the dumps come from the eager step (src/main.cu:253)
+    } else if (s->persistent) {
         if (step_kernel_launch(cfg, step_args(cfg, w, s, 0), s->step_grid, s->stream))
             s->next_token_valid = 1;
     } else if (s->graph) {

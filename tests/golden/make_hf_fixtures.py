@@ -6,6 +6,8 @@ tests/golden/hf_small_qwen3.npz, the small model (SMALL, small_weights(0)), toke
   logits      [len(TOKENS), vocab] fp32: teacher-forced logits at every position (one forward)
   greedy      [GREEDY_STEPS] int32: greedy tokens after PROMPT (model.generate, no sampling)
   greedy_gap  [GREEDY_STEPS] fp32: top-1 minus top-2 logit at each greedy step
+tests/golden/hf_small_qwen3_dumps.npz, the small model's activation dumps (the reference's
+  dump taxonomy, ref/dump.py:39-86) at the positions of TOKENS, as bf16 bits
 tests/golden/hf_qwen3_06b_greedy.npz, the Qwen3-0.6B shapes (QWEN3_06B, qwen3_np_weights(., 0)),
 the bench's 5 seeded prompt ids:
   greedy, greedy_gap  [256]; top_values, top_indices [256, 8]: the 8 largest logits per step
@@ -14,7 +16,7 @@ These pin what no closed form does: the HF fp32/bf16 CPU arithmetic end to end (
 within 2e-2 and the greedy sequence up to near ties). The fixtures are data; this script is the
 only place transformers is imported, and only here (never on the GPU box).
 
-Run from the repository root:  python tests/golden/make_hf_fixtures.py [small] [0.6B]
+Run from the repository root:  python tests/golden/make_hf_fixtures.py [small] [dumps] [0.6B]
 """
 import json
 import os
@@ -90,6 +92,80 @@ def small_fixture():
     print("wrote hf_small_qwen3.npz:", logits.shape, greedy[:8], "min gap", min(gaps))
 
 
+# The tensors of one decoder layer in dump order, with the module whose output (or, marked "in",
+# whose input) holds it; q_rope/k_rope come from the RoPE function (ref/dump.py:39-86 taxonomy).
+LAYER_TAPS = [("attn_norm", "input_layernorm", "out"), ("q_proj", "self_attn.q_proj", "out"),
+              ("k_proj", "self_attn.k_proj", "out"), ("v_proj", "self_attn.v_proj", "out"),
+              ("q_norm", "self_attn.q_norm", "out"), ("k_norm", "self_attn.k_norm", "out"),
+              ("attn_out", "self_attn.o_proj", "in"), ("o_proj", "self_attn.o_proj", "out"),
+              ("attn_resid", "post_attention_layernorm", "in"),
+              ("mlp_norm", "post_attention_layernorm", "out"), ("gate", "mlp.gate_proj", "out"),
+              ("up", "mlp.up_proj", "out"), ("mlp_act", "mlp.down_proj", "in"),
+              ("down", "mlp.down_proj", "out"), ("out", "", "out")]
+
+
+def small_dumps_fixture():
+    """tests/golden/hf_small_qwen3_dumps.npz: every dumped tensor of the small model at the
+    positions of TOKENS (one teacher-forced forward; causal, so row t is position t's decode),
+    as bf16 bits [len(TOKENS), width] (HF computes them all in bf16)."""
+    import torch
+    from transformers.models.qwen3 import modeling_qwen3
+
+    from conftest import SMALL, small_weights
+
+    model = hf_model(SMALL, small_weights(0))
+    acts, hooks = {}, []
+
+    def rows(t):
+        return t[0].detach().to(torch.bfloat16).reshape(t.shape[1], -1).contiguous()
+
+    def tap(name, where):
+        if where == "in":
+            return lambda mod, args: acts.__setitem__(name, rows(args[0]))
+        return lambda mod, args, out: acts.__setitem__(name, rows(out[0] if isinstance(out, tuple) else out))
+
+    inner = model.model
+    hooks.append(inner.embed_tokens.register_forward_hook(tap("embed", "out")))
+    layer_of = {}
+    for i, layer in enumerate(inner.layers):
+        for name, path, where in LAYER_TAPS:
+            mod = layer
+            for part in filter(None, path.split(".")):
+                mod = getattr(mod, part)
+            fn = tap(f"L{i:02d}.{name}", where)
+            hooks.append(mod.register_forward_pre_hook(fn) if where == "in"
+                         else mod.register_forward_hook(fn))
+        layer_of[id(layer.self_attn)] = i
+        hooks.append(layer.self_attn.register_forward_pre_hook(
+            lambda mod, args, kwargs: acts.__setitem__("_layer", layer_of[id(mod)]),
+            with_kwargs=True))
+    hooks.append(inner.norm.register_forward_hook(tap("final_norm", "out")))
+    hooks.append(model.lm_head.register_forward_hook(tap("logits", "out")))
+    rope = modeling_qwen3.apply_rotary_pos_emb
+
+    def rope_tap(q, k, cos, sin, *a, **kw):
+        qe, ke = rope(q, k, cos, sin, *a, **kw)
+        p = f"L{acts['_layer']:02d}"
+        acts[p + ".q_rope"] = rows(qe.transpose(1, 2))  # [batch, seq, heads, dim]
+        acts[p + ".k_rope"] = rows(ke.transpose(1, 2))
+        return qe, ke
+
+    modeling_qwen3.apply_rotary_pos_emb = rope_tap
+    try:
+        with torch.no_grad():
+            model(torch.tensor([TOKENS]))
+    finally:
+        modeling_qwen3.apply_rotary_pos_emb = rope
+        for h in hooks:
+            h.remove()
+    acts.pop("_layer")
+    n_expected = 1 + SMALL["n_layers"] * (len(LAYER_TAPS) + 2) + 2
+    assert len(acts) == n_expected, (len(acts), n_expected)
+    out = {name: t.view(torch.int16).numpy().view(np.uint16) for name, t in acts.items()}
+    np.savez_compressed(os.path.join(HERE, "hf_small_qwen3_dumps.npz"), **out)
+    print("wrote hf_small_qwen3_dumps.npz:", len(out), "tensors")
+
+
 def qwen06b_fixture():
     import torch
     import transformers
@@ -121,8 +197,10 @@ def qwen06b_fixture():
 
 
 if __name__ == "__main__":
-    which = sys.argv[1:] or ["small", "0.6B"]
+    which = sys.argv[1:] or ["small", "dumps", "0.6B"]
     if "small" in which:
         small_fixture()
+    if "dumps" in which:
+        small_dumps_fixture()
     if "0.6B" in which:
         qwen06b_fixture()

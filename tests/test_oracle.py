@@ -459,3 +459,21 @@ def test_sample_against_double_cdf(oracle):
             i = oracle.sample(row, inv_temp, float(u))
             lo = cdf[i - 1] if i > 0 else 0.0
             assert lo - 1e-5 <= u <= cdf[i] + 1e-5, (trial, u, i, lo, cdf[i])
+
+
+def test_hf_dump_fixture_wiring(oracle):
+    """The HF dump fixture holds what its names say (ref/dump.py:101-108): the embedding rows of
+    the tokens, and each residual add exactly bf16(x + y)."""
+    from conftest import SMALL, small_weights
+    here = os.path.dirname(os.path.abspath(__file__))
+    ref = np.load(os.path.join(here, "golden", "hf_small_qwen3_dumps.npz"))
+    tokens = hf_fixture()[1]["tokens"]
+    emb = small_weights(0)["model.embed_tokens.weight"]
+    assert np.array_equal(ref["embed"], emb[tokens])
+    v = {n: bf16_vals(ref[n]).astype(np.float32) for n in ref.files}
+    x = v["embed"]
+    for l in range(SMALL["n_layers"]):
+        p = f"L{l:02d}."
+        assert np.array_equal(ref[p + "attn_resid"], bf16_bits(x + v[p + "o_proj"]))
+        x = v[p + "out"]
+        assert np.array_equal(ref[p + "out"], bf16_bits(v[p + "attn_resid"] + v[p + "down"]))

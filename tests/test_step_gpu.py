@@ -157,6 +157,66 @@ def test_sample_temperature_step(small_model, oracle):
         assert dec.sample_temperature(temp, coin) == oracle.sample(lg, np.float32(1.0 / temp), coin)
 
 
+# ref/compare.py:13-18: worst-row relative L2 error per dumped tensor (embed and layer 0 held
+# tighter), and the near-tie rule for the logits' argmax
+DUMP_TOL_FIRST, DUMP_TOL = 0.02, 0.15
+
+
+def test_small_model_dumps_match_hf(small_model, tmp_path):
+    """Activation dumps (include/llm_amd/dump.h) of the eager step over the fixture's tokens
+    against HF transformers' own tensors at the same points (tests/golden/hf_small_qwen3_dumps.npz,
+    the reference's dump taxonomy): every tensor present with one row per position, worst-row
+    relative L2 within ref/compare.py's tolerances, embedding rows bit-exact, the residual adds
+    exactly bf16(x + y) (ref/dump.py:101-108), and the logits' argmax equal up to a near tie."""
+    import json
+    import os
+    import llm_inference_amd as lia
+    ident("dumps vs HF")
+    dec, _ = small_model
+    here = os.path.dirname(os.path.abspath(__file__))
+    ref = np.load(os.path.join(here, "golden", "hf_small_qwen3_dumps.npz"))
+    tokens = json.loads(str(np.load(os.path.join(here, "golden", "hf_small_qwen3.npz"))["meta"]))["tokens"]
+    d = tmp_path / "dumps"
+    lia.dump_open(d)
+    try:
+        for pos, tok in enumerate(tokens):
+            dec.forward(tok, pos)
+            dec.sample_argmax()
+    finally:
+        lia.dump_close()
+    mine = {}
+    for name in ref.files:
+        raw = np.fromfile(d / f"{name}.bin", dtype=np.float32)
+        width = ref[name].shape[1]
+        assert raw.size == len(tokens) * width, (name, raw.size)
+        mine[name] = raw.reshape(len(tokens), width).astype(np.float64)
+    assert sorted(mine) == sorted(ref.files)
+    assert len([f for f in os.listdir(d) if f.endswith(".bin")]) == len(ref.files)
+    worst = {}
+    for name in ref.files:
+        r = bf16_vals(ref[name]).astype(np.float64)
+        err = (np.linalg.norm(mine[name] - r, axis=1) / np.linalg.norm(r, axis=1)).max()
+        tol = DUMP_TOL_FIRST if name == "embed" or name.startswith("L00.") else DUMP_TOL
+        assert err <= tol, (name, float(err))
+        worst[name] = float(err)
+    assert np.array_equal(mine["embed"], bf16_vals(ref["embed"]).astype(np.float64))
+
+    def bf16_add(a, b):
+        return bf16_vals(bf16_bits((a + b).astype(np.float32))).astype(np.float64)
+    x = mine["embed"]
+    for l in range(SMALL["n_layers"]):
+        p = f"L{l:02d}."
+        assert np.array_equal(mine[p + "attn_resid"], bf16_add(x, mine[p + "o_proj"]))
+        x = mine[p + "out"]
+        assert np.array_equal(x, bf16_add(mine[p + "attn_resid"], mine[p + "down"]))
+    lg, rl = mine["logits"], bf16_vals(ref["logits"]).astype(np.float64)
+    for t in range(len(tokens)):
+        a, b = int(lg[t].argmax()), int(rl[t].argmax())
+        assert a == b or rl[t, b] - rl[t, a] <= TIE_GAP, (t, a, b)
+    top = sorted(worst.items(), key=lambda kv: -kv[1])[:3]
+    print("[case] worst tensors: " + ", ".join(f"{n} {e:.4f}" for n, e in top), flush=True)
+
+
 def test_small_model_matches_hf_fixture(small_model):
     """The GPU step (loaded through the safetensors loader) against HF transformers' Qwen3 on the
     same weights (tests/golden/hf_small_qwen3.npz: bf16, eager attention, CPU): teacher-forced
