@@ -23,6 +23,8 @@
 #include <limits.h>
 #include <string.h>
 
+#include <type_traits>
+
 #include "common.h"
 #include "internal.h"
 #include "rope.h"
@@ -770,6 +772,9 @@ enum {
     PF_AFTER_COMPUTE = 2,   // down rows after the gate/up rows, q/k/v after the down rows
 };
 
+// The roles a token loop is compiled for.
+enum { ROLE_ATTN = 0, ROLE_MATRIX = 1, ROLE_EITHER = 2 };
+
 template <class S>
 __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
     constexpr int H = S::H, I = S::I, D = 128, QD = S::HQ * D, KVD = S::HKV * D;
@@ -854,19 +859,29 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
     // [R, R) and loads row R - 1 (a cache hit after its owner's load). A request made on some
     // paths only would leave the registers to be merged where the paths join, and the copy
     // made there waits for the load (and, loads completing in order, for every earlier one).
+    //
+    // The token loop is instantiated per role: ROLE_ATTN (the attention workgroups),
+    // ROLE_MATRIX, or ROLE_EITHER (one loop for both, the role a run-time branch). With
+    // S::SPLIT_ROLES the two roles get their own loops, so the matrix role's loop-carried q/k/v
+    // prefetch is not live through the attention code.
+    auto run = [&](auto role) __attribute__((always_inline)) {
+    constexpr int ROLE = decltype(role)::value;
+    const bool attn = ROLE == ROLE_ATTN || (ROLE == ROLE_EITHER && attn_wg);
     // The first layer's q/k/v rows of the next token, requested before the token is known
     // (by the last layer of the previous token after the first).
     Rows<NCH, S::B_QKV> pf_qkv;
     NormW<H> nq;  // attn_norm weights of the coming q/k/v phase
-    nq.load(klayer(kargs(), 0).attn_norm);
-    pf_qkv.load(qkv_row(klayer(kargs(), 0)), q0, q1);
+    if (ROLE != ROLE_ATTN) {
+        nq.load(klayer(kargs(), 0).attn_norm);
+        pf_qkv.load(qkv_row(klayer(kargs(), 0)), q0, q1);
+    }
 
     for (int step = 0; step < n_tokens; step++, pos++) {
     const unsigned sq0 = seq0 + step * seq_step;  // this token's first tag
     stamp<S>(0, step);
     // tags of layer l: seq q|k|v, seq+1 attention, seq+2 x after o, seq+3 SwiGLU, seq+4 x
     // after down, with seq = sq0 + PHASES * l; the next token: sq0 + PHASES * n_layers
-    if (attn_wg) {
+    if (attn) {
         // ---- QK-norm + RoPE + KV write + attention, one query head per workgroup
         for (int l = 0; l < n_layers; l++) {
             const unsigned seq = sq0 + PHASES * l;
@@ -1118,6 +1133,15 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
         }
     }
     }
+    };
+    if constexpr (S::SPLIT_ROLES) {
+        if (attn_wg)
+            run(std::integral_constant<int, ROLE_ATTN>{});
+        else
+            run(std::integral_constant<int, ROLE_MATRIX>{});
+    } else {
+        run(std::integral_constant<int, ROLE_EITHER>{});
+    }
 }
 
 }  // namespace
@@ -1139,8 +1163,12 @@ struct Shape {
     static constexpr int B_GU = H <= 1024 ? 2 : 1;
     static constexpr int B_DOWN = 1;
     static constexpr int B_LM = H <= 1024 ? 8 : (H <= 2048 ? 4 : 2);
-    static constexpr int PF_D = H <= 1024 ? PF_WITH_ATTENTION : PF_AFTER_COMPUTE;
+    // 1.7B: the down rows with attention 1050 -> 1075 tokens/s, the q/k/v rows too 1005
+    static constexpr int PF_D = H <= 2048 ? PF_WITH_ATTENTION : PF_AFTER_COMPUTE;
     static constexpr int PF_QKV = H <= 1024 ? PF_WITH_ATTENTION : PF_AFTER_COMPUTE;
+    // separate token loops for the two roles: 0.6B +1.7%; 1.7B -1.8% (its one shared loop
+    // spills the q/k/v prefetch to scratch memory, yet measures faster)
+    static constexpr bool SPLIT_ROLES = H != 2048;
     // wave 0 of every workgroup stages the vectors and owns no matrix rows (so no weight load
     // is in flight in the polling wave); the larger shapes' vectors need every wave to poll
     static constexpr bool POLLER = false;
