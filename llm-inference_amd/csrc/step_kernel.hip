@@ -1219,8 +1219,8 @@ bool step_kernel_supported(const Config *cfg, int max_seq) {
            step_grid_fits(cfg, step_kernel_grid());
 }
 
-// Measured on MI355X, 5-token prompt then 128 tokens: 0.6B 2244 tokens/s (step kernel) against
-// 1187 (hipGraph), 1.7B 1057 against 859, 4B 321 against 480: the 4B layers stream 202 MB
+// Measured on MI355X, 5-token prompt then 128 tokens: 0.6B 2330 tokens/s (step kernel) against
+// 1179 (hipGraph), 1.7B 1059 against 856, 4B 356 against 479: the 4B layers stream 202 MB
 // each, which the per-kernel GEMVs of the graph read faster than the step kernel's row batches.
 bool step_kernel_preferred(const Config *cfg) { return cfg->hidden_size <= 2048; }
 
