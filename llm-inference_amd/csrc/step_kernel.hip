@@ -37,8 +37,9 @@ namespace {
 constexpr int WAVES = 8;                   // waves per workgroup
 constexpr int THREADS = 64 * WAVES;
 constexpr long long SPIN_LIMIT = 1 << 22;  // polls before a wait gives up (~ seconds)
-// Pause between polls (s_sleep units of 64 clocks): polling traffic slows the memory side.
-constexpr int POLL_SLEEP = 1;
+// Pause between polls (s_sleep units of 64 clocks). None: at 0.6B polling without a pause
+// measured 0.3% faster than 64 clocks and 1% faster than 128.
+constexpr int POLL_SLEEP = 0;
 constexpr int PHASES = 5;                  // tagged vectors written per layer
 
 // ---------------------------------------------------------------- coherent access
@@ -156,7 +157,7 @@ __device__ __forceinline__ void stage_pairs(Src src, uint32_t tag, uint32_t *dst
                 __hip_atomic_store(gptr(err), 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
             }
-            __builtin_amdgcn_s_sleep(POLL_SLEEP);
+            if constexpr (POLL_SLEEP > 0) __builtin_amdgcn_s_sleep(POLL_SLEEP);
         }
 #pragma unroll
         for (int j = 0; j < P; j++) {
