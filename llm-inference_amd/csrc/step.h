@@ -13,9 +13,10 @@ struct LayerDev {
 // 32-bit word (bf16 bits << 16) | tag, where tag (1..65535) names the phase that wrote it.
 // A consumer polls the words it needs until every tag is the expected one; there is no grid
 // barrier. tx: residual stream [H], tqkv: q|k|v [QD + 2 KVD], tattn: attention output [QD],
-// thb: SwiGLU output [I]. The vectors read by many workgroups (tx, tattn, thb) are written in
-// STEP_REPLICAS copies, step_replica_stride(n) words apart, and workgroup b reads copy
-// b % STEP_REPLICAS: fewer pollers per cache line make a written value visible sooner.
+// thb: SwiGLU output [I]. The vectors read by many workgroups (tx, tattn, thb) have room for
+// STEP_REPLICAS copies, step_replica_stride(n) words apart; a model shape writes the first
+// R <= STEP_REPLICAS of them and workgroup b reads copy b % R: fewer pollers per cache line make
+// a written value visible sooner, more copies cost the writers more stores.
 constexpr int STEP_REPLICAS = 8;
 constexpr size_t step_replica_stride(size_t n) { return (n + 1023) / 1024 * 1024; }
 

@@ -96,20 +96,23 @@ __device__ __forceinline__ void put_tagged(uint32_t *v, int i, uint32_t bits, ui
                        __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Element i of a replicated tagged vector of n elements, into every copy.
-template <int N>
+// Element i of a replicated tagged vector of n elements, into each of its first COPIES copies
+// (at most STEP_REPLICAS; the workgroups read only those).
+template <int N, int COPIES>
 __device__ __forceinline__ void put_tagged_all(uint32_t *v, int i, uint32_t bits, uint32_t tag) {
+    static_assert(COPIES >= 1 && COPIES <= STEP_REPLICAS, "copies");
     constexpr int STRIDE = (int)step_replica_stride(N);
 #pragma unroll
-    for (int q = 0; q < STEP_REPLICAS; q++) put_tagged(v + q * STRIDE, i, bits, tag);
+    for (int q = 0; q < COPIES; q++) put_tagged(v + q * STRIDE, i, bits, tag);
 }
 
 // Rows [r0, r1) of a replicated tagged vector, staged in LDS as tagged words by the waves that
 // computed them, written to every copy by one wave: consecutive lanes on consecutive words of a
 // copy, so each copy's run of rows goes out in one store instruction instead of one single-lane
 // store per row and copy.
-template <int N, int COPIES = STEP_REPLICAS>
+template <int N, int COPIES>
 __device__ __forceinline__ void publish_rows(uint32_t *v, const uint32_t *stage, int r0, int r1) {
+    static_assert(COPIES >= 1 && COPIES <= STEP_REPLICAS, "copies");
     constexpr int STRIDE = (int)step_replica_stride(N);
     const int n = r1 - r0;
     for (int idx = tid_x() & 63; idx < n * COPIES; idx += 64) {
@@ -119,10 +122,11 @@ __device__ __forceinline__ void publish_rows(uint32_t *v, const uint32_t *stage,
     }
 }
 
-// The copy of a replicated tagged vector of n elements that this workgroup reads.
-template <int N>
+// The copy of a replicated tagged vector of n elements, written in COPIES copies, that this
+// workgroup reads.
+template <int N, int COPIES>
 __device__ __forceinline__ const uint32_t *my_copy(const uint32_t *v) {
-    return v + (blockIdx.x % STEP_REPLICAS) * (int)step_replica_stride(N);
+    return v + (blockIdx.x % COPIES) * (int)step_replica_stride(N);
 }
 
 // Polls the 64-bit words src(p) (two tagged elements each) for pairs p < PAIRS until both tags
@@ -732,7 +736,7 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
         }
         if (!last) __syncthreads();  // the quarters are read before the next round rewrites them
     }
-    if (threadIdx.x < D) put_tagged_all<QD>(a.tattn, h * D + threadIdx.x, f2bf(out_d), tag_out);
+    if (threadIdx.x < D) put_tagged_all<QD, S::REPLICAS>(a.tattn, h * D + threadIdx.x, f2bf(out_d), tag_out);
 }
 
 // ---------------------------------------------------------------- the step
@@ -916,7 +920,7 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                 if (l == 0) {
                     stage_plain<H>(kargs().embed + (size_t)token * H, sm.vec);
                 } else {
-                    stage_vector<H, OW>(my_copy<H>(kargs().tx), tag_of(seq - 1), sm.vec,
+                    stage_vector<H, OW>(my_copy<H, S::REPLICAS>(kargs().tx), tag_of(seq - 1), sm.vec,
                                         kargs().error_flag);
                 }
             }
@@ -958,7 +962,7 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
             }
             // ---- o rows + residual
             if (wg_o)
-                stage_vector<QD, OW>(my_copy<QD>(kargs().tattn), tag_of(seq + 1), sm.vec,
+                stage_vector<QD, OW>(my_copy<QD, S::REPLICAS>(kargs().tattn), tag_of(seq + 1), sm.vec,
                                      kargs().error_flag);
             stamp<S>(2 + 4 * l, step);
             stamp_wg(l, n_layers, 2, step);
@@ -972,12 +976,12 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                         residual(out_stage, wr0, tag_of(seq + 2)), &xown);
                 }
                 __syncthreads();
-                if ((tid_x() >> 6) == FW) publish_rows<H>(kargs().tx, out_stage, wr0, wr1);
+                if ((tid_x() >> 6) == FW) publish_rows<H, S::REPLICAS>(kargs().tx, out_stage, wr0, wr1);
             }
             stamp_wg(l, n_layers, 3, step);
             // ---- rmsnorm + gate/up rows + SwiGLU
             if (wg_g)
-                stage_vector<H, OW>(my_copy<H>(kargs().tx), tag_of(seq + 2), sm.vec,
+                stage_vector<H, OW>(my_copy<H, S::REPLICAS>(kargs().tx), tag_of(seq + 2), sm.vec,
                                     kargs().error_flag);
             stamp<S>(3 + 4 * l, step);
             stamp_wg(l, n_layers, 4, step);
@@ -998,14 +1002,14 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                                          [=](int r, float g, float u) {
                     const bf16 gb = (bf16)f2bf(g), ub = (bf16)f2bf(u);
                     const float s = round_bf(silu_f32(bf2f(gb)));
-                    put_tagged_all<I>(hb, r, f2bf(s * bf2f(ub)), tag);
+                    put_tagged_all<I, S::REPLICAS>(hb, r, f2bf(s * bf2f(ub)), tag);
                 });
             }
             stamp_wg(l, n_layers, 5, step);
             if constexpr (S::PF_D == PF_AFTER_COMPUTE) pf_d.load(d_row(klayer(kargs(), l)), o0, o1);
             // ---- down rows + residual
             if (wg_o)
-                stage_vector<I, OW>(my_copy<I>(kargs().thb), tag_of(seq + 3), sm.vec,
+                stage_vector<I, OW>(my_copy<I, S::REPLICAS>(kargs().thb), tag_of(seq + 3), sm.vec,
                                     kargs().error_flag);
             stamp<S>(4 + 4 * l, step);
             stamp_wg(l, n_layers, 6, step);
@@ -1018,7 +1022,7 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                         residual(out_stage, wr0, tag_of(seq + 4)), &xown);
                 }
                 __syncthreads();
-                if ((tid_x() >> 6) == FW) publish_rows<H>(kargs().tx, out_stage, wr0, wr1);
+                if ((tid_x() >> 6) == FW) publish_rows<H, S::REPLICAS>(kargs().tx, out_stage, wr0, wr1);
             }
             stamp_wg(l, n_layers, 7, step);
             if constexpr (S::PF_QKV == PF_AFTER_COMPUTE) {
@@ -1040,7 +1044,7 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
         NormW<H> nf{};  // final_norm weights
         nf.load(kargs().final_norm);
         batch.load(lm_row, r0, r1);
-        stage_vector<H, OW>(my_copy<H>(kargs().tx), tag_of(seq_end - 1), sm.vec,
+        stage_vector<H, OW>(my_copy<H, S::REPLICAS>(kargs().tx), tag_of(seq_end - 1), sm.vec,
                             kargs().error_flag);
         stamp<S>(1 + 4 * n_layers, step);
         wg_rmsnorm<H>(sm.vec, nf, kargs().eps, &norm_inv);
@@ -1169,6 +1173,9 @@ struct Shape {
     static constexpr int B_GU = H <= 1024 ? 2 : 1;
     static constexpr int B_DOWN = 1;
     static constexpr int B_LM = H <= 2048 ? 4 : 2;  // 0.6B: 4 rows +0.4% over 8, 16 spills
+    // copies of x, the attention output and the SwiGLU output (at most STEP_REPLICAS):
+    // 0.6B 8 (4: -0.2%, 16: -2.6%), 1.7B 4 (+4.2% over 8)
+    static constexpr int REPLICAS = H <= 1024 ? 8 : 4;
     // 1.7B: the down rows with attention 1050 -> 1075 tokens/s, the q/k/v rows too 1005
     static constexpr int PF_D = H <= 2048 ? PF_WITH_ATTENTION : PF_AFTER_COMPUTE;
     static constexpr int PF_QKV = H <= 1024 ? PF_WITH_ATTENTION : PF_AFTER_COMPUTE;
