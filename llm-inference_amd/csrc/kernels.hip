@@ -1110,46 +1110,53 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnArgs a) {
     }
 }
 
-// Pass 3: out = bf16(block partials added in block order), one workgroup per query head. The
-// additions are sequential, the loads are not: the head's partials are staged in LDS by all 256
-// threads (every 16-byte load of a chunk of CB blocks in flight at once), then thread d adds
-// column d in block order, 16 LDS reads at a time.
+// Pass 3: out = bf16(block partials added in block order). A workgroup takes COMBINE_COLS
+// columns of one query head (D / COMBINE_COLS workgroups per head, so the loads spread over
+// more CUs). The additions are sequential, the loads are not: the columns' partials are staged
+// in LDS by all 256 threads (every 16-byte load of a chunk of CB blocks in flight at once), then
+// thread c adds column c in block order, 16 LDS reads at a time.
+constexpr int COMBINE_COLS = 32;
 template <int D>
 __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
-    constexpr int CB = 32768 / D;  // blocks per LDS chunk (128 KB: one chunk up to 16384 positions at D = 128)
-    __shared__ float part[CB * D];
-    const int h = blockIdx.x;
+    constexpr int CC = COMBINE_COLS, Q = CC / 4;  // columns; 16-byte loads per block row
+    constexpr int CB = 256;                      // blocks per LDS chunk (32 KB, 16384 positions)
+    static_assert(D % CC == 0, "columns per workgroup");
+    __shared__ float part[CB * CC];
+    const int h = blockIdx.x / (D / CC), c0 = (blockIdx.x % (D / CC)) * CC;
     const int n = *a.d_pos + 1;
     const int nb = (n + ATT_B - 1) / ATT_B;
-    const float *src = a.partial + (size_t)h * a.max_blocks * D;
+    const float *src = a.partial + (size_t)h * a.max_blocks * D + c0;
     float acc = 0.0f;
     for (int b0 = 0; b0 < nb; b0 += CB) {
         const int cnt = min(CB, nb - b0);
         if (b0 > 0) __syncthreads();  // the previous chunk has been added
-        const u32x4 *s4 = (const u32x4 *)(src + (size_t)b0 * D);
-        constexpr int PER = CB * D / 4 / 256;  // 16-byte loads per thread for a full chunk
-        const int n4 = cnt * D / 4;
+        constexpr int PER = CB * Q / 256;  // 16-byte loads per thread for a full chunk
+        const int n4 = cnt * Q;
         u32x4 v4[PER];
 #pragma unroll
-        for (int j = 0; j < PER; j++) v4[j] = s4[min((int)threadIdx.x + 256 * j, n4 - 1)];
+        for (int j = 0; j < PER; j++) {
+            // load i: block b0 + i / Q, columns c0 + 4 (i % Q) .. + 3
+            const int i = min((int)threadIdx.x + 256 * j, n4 - 1);
+            v4[j] = *(const u32x4 *)(src + (size_t)(b0 + i / Q) * D + 4 * (i % Q));
+        }
 #pragma unroll
         for (int j = 0; j < PER; j++)
             if ((int)threadIdx.x + 256 * j < n4) ((u32x4 *)part)[threadIdx.x + 256 * j] = v4[j];
         __syncthreads();
-        if (threadIdx.x < D) {
+        if (threadIdx.x < CC) {
             // 16 LDS reads in flight, then their additions in order
-            const int d = threadIdx.x;
+            const int c = threadIdx.x;
             for (int j0 = 0; j0 < cnt; j0 += 16) {
                 float v[16];
 #pragma unroll
-                for (int j = 0; j < 16; j++) v[j] = part[min(j0 + j, cnt - 1) * D + d];
+                for (int j = 0; j < 16; j++) v[j] = part[min(j0 + j, cnt - 1) * CC + c];
 #pragma unroll
                 for (int j = 0; j < 16; j++)
                     if (j0 + j < cnt) acc = (b0 + j0 + j == 0) ? v[j] : acc + v[j];
             }
         }
     }
-    if (threadIdx.x < D) a.out[(size_t)h * D + threadIdx.x] = (bf16)f2bf(acc);
+    if (threadIdx.x < CC) a.out[(size_t)h * D + c0 + threadIdx.x] = (bf16)f2bf(acc);
 }
 
 template <int D, int REP>
@@ -1158,7 +1165,7 @@ static void launch_attention_t(const AttnArgs &a, int grid, hipStream_t stream) 
     if (!LAUNCH_OK()) return;
     attn_pv_kernel<D, REP><<<grid, 256, 0, stream>>>(a);
     if (!LAUNCH_OK()) return;
-    attn_combine_kernel<D><<<a.n_heads, 256, 0, stream>>>(a);
+    attn_combine_kernel<D><<<a.n_heads * (D / COMBINE_COLS), 256, 0, stream>>>(a);
     LAUNCH_OK();
 }
 
