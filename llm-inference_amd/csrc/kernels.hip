@@ -1039,10 +1039,12 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnArgs a) {
                     mv[c] = st[2 * bi];
                     sv[c] = st[2 * bi + 1];
                 }
+                // a max is exact in any order: over the lane's chunks first, then one wave_max
+                float ml = -__builtin_huge_valf();
 #pragma unroll
                 for (int c = 0; c < MAXC; c++)
-                    if (c * 64 < nb)
-                        M = fmaxf(M, wave_max(c * 64 + lane < nb ? mv[c] : -__builtin_huge_valf()));
+                    if (c * 64 + lane < nb) ml = fmaxf(ml, mv[c]);
+                M = wave_max(ml);
 #pragma unroll
                 for (int c = 0; c < MAXC; c++)
                     if (c * 64 < nb) {
