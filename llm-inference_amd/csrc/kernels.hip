@@ -1016,22 +1016,65 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnArgs a) {
     const int kv_dim = a.n_kv_heads * D;
     for (int item = blockIdx.x; item < nb * a.n_kv_heads; item += gridDim.x) {
         const int b = item / a.n_kv_heads, g = item - b * a.n_kv_heads;
+        // The first head of this wave (r = w): its score and block statistics are requested
+        // before the values. Loads complete in order, so the statistics chain then waits only
+        // for them and runs while the values stream. Unconditional (clamped indices), so no
+        // branch joins before the value requests.
+        constexpr int MAXC = 4;  // chunks of 64 block statistics held in registers
+        const int r_first = w < REP ? w : 0;
+        float mv0[MAXC], sv0[MAXC], s_t0;
+        {
+            const int h = g * REP + r_first;
+            const float *st = a.stats + (size_t)h * a.max_blocks * 2;
+            s_t0 = a.scores[(size_t)h * a.max_seq + min(b * ATT_B + lane, n - 1)];
+#pragma unroll
+            for (int c = 0; c < MAXC; c++) {
+                const int bi = min(c * 64 + lane, nb - 1);
+                mv0[c] = st[2 * bi];
+                sv0[c] = st[2 * bi + 1];
+            }
+        }
+        // every lane requests a value row (positions past n clamped to n - 1: the PV loop skips
+        // those slots), so no load sits on some paths only and no wait is made conservative
         u32x4 vv[ITERS];
 #pragma unroll
         for (int it = 0; it < ITERS; it++) {
-            const int t = b * ATT_B + w * PER_WAVE + it * PPW + G;
-            vv[it] = t < n ? ld16_nt(a.vc + (size_t)t * kv_dim + g * D + 8 * L) : u32x4{0, 0, 0, 0};
+            const int t = min(b * ATT_B + w * PER_WAVE + it * PPW + G, n - 1);
+            vv[it] = ld16_nt(a.vc + (size_t)t * kv_dim + g * D + 8 * L);
+        }
+        // The first head's probabilities from those statistics (nb <= 64 * MAXC: the max is exact
+        // in any order, so over the lane's chunks first and then one wave_max; the chunk sums
+        // added in order), computed by every wave with no branch, so the requests above are not
+        // moved below the value requests. Kept only by a wave that has a head, for nb <= 64 MAXC.
+        float p0;
+        {
+            float ml = -__builtin_huge_valf();
+#pragma unroll
+            for (int c = 0; c < MAXC; c++) ml = c * 64 + lane < nb ? fmaxf(ml, mv0[c]) : ml;
+            const float M = wave_max(ml);
+            float cs[MAXC];
+#pragma unroll
+            for (int c = 0; c < MAXC; c++)
+                cs[c] = wave_sum(c * 64 + lane < nb ? sv0[c] * exp_f32(mv0[c] - M) : 0.0f);
+            float sum = cs[0];
+#pragma unroll
+            for (int c = 1; c < MAXC; c++) sum = c * 64 < nb ? sum + cs[c] : sum;
+            p0 = b * ATT_B + lane < n ? round_bf(exp_f32(s_t0 - M) / sum) : 0.0f;
         }
         for (int r = w; r < REP; r += 4) {
+            if (r == w && nb <= 64 * MAXC) {
+                p_s[r][lane] = p0;
+                continue;
+            }
+            // a second head of the wave (REP = 8), or more than 64 * MAXC blocks
             const int h = g * REP + r;
             const float *st = a.stats + (size_t)h * a.max_blocks * 2;
             const int t = b * ATT_B + lane;
             const float s_t = a.scores[(size_t)h * a.max_seq + min(t, n - 1)];
             float M = -__builtin_huge_valf(), sum = 0.0f;
-            constexpr int MAXC = 4;  // chunks of 64 block statistics held in registers
             if (nb <= 64 * MAXC) {
                 // every statistic requested at once (clamped indices, no branch around the
-                // loads), then the same max and in-order chunk sums as below
+                // loads), then the same max and in-order chunk sums as p0's
                 float mv[MAXC], sv[MAXC];
 #pragma unroll
                 for (int c = 0; c < MAXC; c++) {
@@ -1039,7 +1082,6 @@ __global__ __launch_bounds__(256) void attn_pv_kernel(AttnArgs a) {
                     mv[c] = st[2 * bi];
                     sv[c] = st[2 * bi + 1];
                 }
-                // a max is exact in any order: over the lane's chunks first, then one wave_max
                 float ml = -__builtin_huge_valf();
 #pragma unroll
                 for (int c = 0; c < MAXC; c++)
