@@ -310,9 +310,16 @@ static bool check_step_error(const Config *cfg, RunState *s) {
 // src/forward.cu:196-204
 extern "C" void capture_graph(const Config *cfg, const Weights *w, RunState *s) {
     StepCtx c{cfg, w, s};
+    // Both captured graphs hold the weight pointers of the call that captured them: a new
+    // capture (new weights, or a new step mode) drops them, and generate_greedy captures its
+    // loop graph again from the current weights when it next needs it.
     if (s->graph) {
         HIP_OK(hipGraphExecDestroy(s->graph));
         s->graph = nullptr;
+    }
+    if (s->loop_graph) {
+        HIP_OK(hipGraphExecDestroy(s->loop_graph));
+        s->loop_graph = nullptr;
     }
     s->persistent = 0;
     // while dumping, the step runs eagerly (the reference captures only without --dump,
@@ -386,6 +393,34 @@ extern "C" int sample_argmax(const Config *cfg, RunState *s) {
     return token;
 }
 
+// token_out holds at least n tokens (a larger buffer drops the loop graph, which captured the
+// old buffer's address).
+static bool ensure_token_capacity(RunState *s, int n) {
+    if (s->token_capacity >= n) return true;
+    if (s->token_out) HIP_OK(hipFree(s->token_out));
+    s->token_out = nullptr;
+    s->token_capacity = 0;
+    if (s->loop_graph) {
+        HIP_OK(hipGraphExecDestroy(s->loop_graph));
+        s->loop_graph = nullptr;
+    }
+    const int cap = n < 256 ? 256 : n;
+    if (!dmalloc((void **)&s->token_out, (size_t)cap * 4)) return false;
+    s->token_capacity = cap;
+    return true;
+}
+
+// The n tokens of a device loop to the host, and the loop's error flag: 0, or -1.
+static int copy_tokens_out(RunState *s, int n, int *out_tokens) {
+    int err = 0;
+    if (!HIP_OK(hipMemcpyAsync(out_tokens, s->token_out, (size_t)n * 4, hipMemcpyDeviceToHost,
+                               s->stream)) ||
+        !HIP_OK(hipMemcpyAsync(&err, s->error_flag, 4, hipMemcpyDeviceToHost, s->stream)) ||
+        !HIP_OK(hipStreamSynchronize(s->stream)))
+        return -1;
+    return err ? -1 : 0;
+}
+
 extern "C" int generate_greedy(const Config *cfg, const Weights *w, RunState *s, int token,
                                int pos, int n_steps, int *out_tokens) {
     if (n_steps <= 0) return 0;
@@ -395,13 +430,26 @@ extern "C" int generate_greedy(const Config *cfg, const Weights *w, RunState *s,
                  pos, s->max_seq);
         return -1;
     }
-    if (s->persistent) {
-        if (s->token_capacity < n_steps) {
-            if (s->token_out) HIP_OK(hipFree(s->token_out));
-            int cap = n_steps < 256 ? 256 : n_steps;
-            if (!dmalloc((void **)&s->token_out, (size_t)cap * 4)) return -1;
-            s->token_capacity = cap;
+    if (dump_enabled()) {
+        // While dumping, every step runs eagerly (dumps synchronise and copy to the host, which
+        // a captured graph or the persistent kernel cannot do): one forward + argmax + advance
+        // per token, writing one row per tensor and position.
+        if (!ensure_token_capacity(s, n_steps)) return -1;
+        set_token_pos_kernel<<<1, 64, 0, s->stream>>>(s->next_token, s->pos, token, pos);
+        set_token_pos_kernel<<<1, 64, 0, s->stream>>>(s->error_flag, s->pos_base, 0, pos);
+        if (!LAUNCH_OK()) return -1;
+        for (int i = 0; i < n_steps; i++) {
+            if (!forward_kernels(cfg, w, s)) return -1;
+            argmax_into_next(cfg, s);
+            advance_kernel<<<1, 64, 0, s->stream>>>(s->pos, s->next_token, s->token_out,
+                                                     s->pos_base, s->token_capacity);
+            if (!LAUNCH_OK()) return -1;
         }
+        s->next_token_valid = 1;
+        return copy_tokens_out(s, n_steps, out_tokens);
+    }
+    if (s->persistent) {
+        if (!ensure_token_capacity(s, n_steps)) return -1;
         set_token_pos_kernel<<<1, 64, 0, s->stream>>>(s->next_token, s->pos, token, pos);
         set_token_pos_kernel<<<1, 64, 0, s->stream>>>(s->error_flag, s->pos_base, 0, pos);
         if (!LAUNCH_OK()) return -1;
@@ -415,17 +463,8 @@ extern "C" int generate_greedy(const Config *cfg, const Weights *w, RunState *s,
             return -1;
         return check_step_error(cfg, s) ? 0 : -1;
     }
-    if (s->token_capacity < n_steps || !s->loop_graph) {
-        if (s->token_capacity < n_steps) {
-            if (s->token_out) HIP_OK(hipFree(s->token_out));
-            int cap = n_steps < 256 ? 256 : n_steps;
-            if (!dmalloc((void **)&s->token_out, (size_t)cap * 4)) return -1;
-            s->token_capacity = cap;
-            if (s->loop_graph) {
-                HIP_OK(hipGraphExecDestroy(s->loop_graph));
-                s->loop_graph = nullptr;
-            }
-        }
+    if (!ensure_token_capacity(s, n_steps)) return -1;
+    if (!s->loop_graph) {
         StepCtx c{cfg, w, s};
         if (!capture(s->stream, &s->loop_graph, loop_body, &c)) return -1;
     }
@@ -434,13 +473,8 @@ extern "C" int generate_greedy(const Config *cfg, const Weights *w, RunState *s,
     if (!LAUNCH_OK()) return -1;
     for (int i = 0; i < n_steps; i++)
         if (!HIP_OK(hipGraphLaunch(s->loop_graph, s->stream))) return -1;
-    int err = 0;
-    if (!HIP_OK(hipMemcpyAsync(out_tokens, s->token_out, (size_t)n_steps * 4,
-                               hipMemcpyDeviceToHost, s->stream)) ||
-        !HIP_OK(hipMemcpyAsync(&err, s->error_flag, 4, hipMemcpyDeviceToHost, s->stream)) ||
-        !HIP_OK(hipStreamSynchronize(s->stream)))
-        return -1;
-    return err ? -1 : 0;
+    s->next_token_valid = 1;
+    return copy_tokens_out(s, n_steps, out_tokens);
 }
 
 // ------------------------------------------------------------------------------------------

@@ -1,10 +1,23 @@
-// Checkpoint loading for the gfx950 build: config.json / generation_config.json and
-// safetensors shards (src/loader.cu:105-419 semantics: BF16 only, shapes implied by the config,
-// 16-byte-aligned data offsets, every tensor in the files used, lm_head tied to the embedding
-// when tie_word_embeddings). JSON is read by the small parser below.
+// Checkpoint loading for the gfx950 build: config.json / generation_config.json and the
+// safetensors shards of a model directory.
+//
+// The on-disk rules are the reference's (src/loader.cu:105-419): BF16 tensors only, shapes
+// implied by config.json, data offsets 16-byte aligned, every tensor in the files used except a
+// tied lm_head, lm_head = embedding when tie_word_embeddings. The design is this file's own:
+//   1. config.json is read through a key table (JSON type and Config field per key);
+//   2. every shard header is validated once into a manifest of tensor entries (name -> shard,
+//      dtype, dims, byte range), rejecting malformed numbers before any cast;
+//   3. the tensors the engine needs form a schema generated from the Config (name, dims, the
+//      Weights/LayerWeights slot it fills), bound against the manifest in one pass;
+//   4. only then is device memory touched: ONE allocation receives the schema's tensors, each
+//      on a 256-byte boundary in schema order (the layout synth_weights produces), copied from
+//      the memory-mapped shards.
+// So every format or shape error is reported before any HIP call.
 #include <dirent.h>
 #include <fcntl.h>
 #include <inttypes.h>
+#include <math.h>
+#include <stddef.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -14,6 +27,7 @@
 
 #include <algorithm>
 #include <string>
+#include <unordered_map>
 #include <utility>
 #include <vector>
 
@@ -248,187 +262,350 @@ bool parse_json_file(const std::string &path, JVal *root) {
     return true;
 }
 
-bool json_number(const JVal &root, const char *key, double *v) {
-    const JVal *item = root.get(key);
-    if (!item || item->type != JVal::NUM)
-        return llm_fail("loader: config.json has no number \"%s\"", key);
-    *v = item->num;
+// A JSON number that is an exact non-negative integer no larger than `max` (safetensors
+// offsets and dims, config sizes); anything else is rejected before it is cast.
+bool json_uint(const JVal *v, double max, uint64_t *out) {
+    if (!v || v->type != JVal::NUM) return false;
+    const double d = v->num;
+    if (!(d >= 0.0) || d > max || floor(d) != d) return false;
+    *out = (uint64_t)d;
     return true;
 }
 
 }  // namespace
 
 // ------------------------------------------------------------------------------------------
-// config (src/loader.cu:73-139)
-// ------------------------------------------------------------------------------------------
-
-static bool load_eos_ids(const char *model_dir, Config *cfg) {
-    std::string path = std::string(model_dir) + "/generation_config.json";
-    JVal root;
-    if (!parse_json_file(path, &root)) return false;
-    const JVal *eos = root.get("eos_token_id");
-    cfg->n_eos = 0;
-    if (eos && eos->type == JVal::NUM) {
-        cfg->eos_ids[0] = (int)eos->num;
-        cfg->n_eos = 1;
-    } else if (eos && eos->type == JVal::ARR) {
-        for (const JVal &id : eos->arr) {
-            if (id.type != JVal::NUM || cfg->n_eos == MAX_EOS)
-                return llm_fail("loader: %s: bad \"eos_token_id\"", path.c_str());
-            cfg->eos_ids[cfg->n_eos++] = (int)id.num;
-        }
-    }
-    if (cfg->n_eos == 0) return llm_fail("loader: %s has no \"eos_token_id\"", path.c_str());
-    return true;
-}
-
-extern "C" void load_config(const char *model_dir, Config *cfg) {
-    memset(cfg, 0, sizeof *cfg);
-    std::string path = std::string(model_dir) + "/config.json";
-    JVal root;
-    if (!parse_json_file(path, &root)) return;
-    const struct {
-        const char *key;
-        int *dst;
-    } ints[] = {{"hidden_size", &cfg->hidden_size},
-                {"intermediate_size", &cfg->intermediate_size},
-                {"num_hidden_layers", &cfg->n_layers},
-                {"num_attention_heads", &cfg->n_heads},
-                {"num_key_value_heads", &cfg->n_kv_heads},
-                {"head_dim", &cfg->head_dim},
-                {"vocab_size", &cfg->vocab_size},
-                {"max_position_embeddings", &cfg->max_seq_len}};
-    double v;
-    for (const auto &f : ints) {
-        if (!json_number(root, f.key, &v)) return;
-        *f.dst = (int)v;
-    }
-    if (!json_number(root, "rms_norm_eps", &v)) return;
-    cfg->rms_norm_eps = (float)v;
-    if (!json_number(root, "rope_theta", &v)) return;
-    cfg->rope_theta = (float)v;
-    const JVal *tie = root.get("tie_word_embeddings");
-    if (!tie || tie->type != JVal::BOOL) {
-        llm_fail("loader: config.json has no bool \"tie_word_embeddings\"");
-        return;
-    }
-    cfg->tie_word_embeddings = tie->b ? 1 : 0;
-    if (cfg->n_kv_heads <= 0 || cfg->n_heads % cfg->n_kv_heads != 0) {
-        llm_fail("loader: num_attention_heads must be a multiple of num_key_value_heads");
-        return;
-    }
-    load_eos_ids(model_dir, cfg);
-}
-
-// ------------------------------------------------------------------------------------------
-// safetensors (src/loader.cu:141-380)
+// config.json and generation_config.json
 // ------------------------------------------------------------------------------------------
 
 namespace {
 
-struct Shard {
+enum KeyKind { KEY_INT, KEY_FLOAT, KEY_BOOL };
+
+struct ConfigKey {
+    const char *key;
+    KeyKind kind;
+    size_t field;  // offset of the Config member
+};
+
+// config.json entries the engine reads, in the order they are checked.
+const ConfigKey kConfigKeys[] = {
+    {"hidden_size", KEY_INT, offsetof(Config, hidden_size)},
+    {"intermediate_size", KEY_INT, offsetof(Config, intermediate_size)},
+    {"num_hidden_layers", KEY_INT, offsetof(Config, n_layers)},
+    {"num_attention_heads", KEY_INT, offsetof(Config, n_heads)},
+    {"num_key_value_heads", KEY_INT, offsetof(Config, n_kv_heads)},
+    {"head_dim", KEY_INT, offsetof(Config, head_dim)},
+    {"vocab_size", KEY_INT, offsetof(Config, vocab_size)},
+    {"max_position_embeddings", KEY_INT, offsetof(Config, max_seq_len)},
+    {"rms_norm_eps", KEY_FLOAT, offsetof(Config, rms_norm_eps)},
+    {"rope_theta", KEY_FLOAT, offsetof(Config, rope_theta)},
+    {"tie_word_embeddings", KEY_BOOL, offsetof(Config, tie_word_embeddings)},
+};
+
+bool read_config_key(const JVal &root, const ConfigKey &k, Config *cfg) {
+    const JVal *v = root.get(k.key);
+    char *field = (char *)cfg + k.field;
+    switch (k.kind) {
+    case KEY_BOOL:
+        if (!v || v->type != JVal::BOOL)
+            return llm_fail("loader: config.json has no bool \"%s\"", k.key);
+        *(int *)field = v->b ? 1 : 0;
+        return true;
+    case KEY_FLOAT:
+        if (!v || v->type != JVal::NUM)
+            return llm_fail("loader: config.json has no number \"%s\"", k.key);
+        *(float *)field = (float)v->num;
+        return true;
+    case KEY_INT: {
+        if (!v || v->type != JVal::NUM)
+            return llm_fail("loader: config.json has no number \"%s\"", k.key);
+        uint64_t u;
+        if (!json_uint(v, 2147483647.0, &u))
+            return llm_fail("loader: config.json: \"%s\" must be a non-negative integer", k.key);
+        *(int *)field = (int)u;
+        return true;
+    }
+    }
+    return false;
+}
+
+// eos_token_id: one id or a list of at most MAX_EOS ids.
+bool read_eos(const char *model_dir, Config *cfg) {
+    const std::string path = std::string(model_dir) + "/generation_config.json";
+    JVal root;
+    if (!parse_json_file(path, &root)) return false;
+    const JVal *eos = root.get("eos_token_id");
+    std::vector<const JVal *> ids;
+    if (eos && eos->type == JVal::NUM) ids.push_back(eos);
+    if (eos && eos->type == JVal::ARR)
+        for (const JVal &id : eos->arr) ids.push_back(&id);
+    if (ids.empty()) return llm_fail("loader: %s has no \"eos_token_id\"", path.c_str());
+    if (ids.size() > MAX_EOS) return llm_fail("loader: %s: bad \"eos_token_id\"", path.c_str());
+    cfg->n_eos = 0;
+    for (const JVal *id : ids) {
+        uint64_t u;
+        if (!json_uint(id, 2147483647.0, &u))
+            return llm_fail("loader: %s: bad \"eos_token_id\"", path.c_str());
+        cfg->eos_ids[cfg->n_eos++] = (int)u;
+    }
+    return true;
+}
+
+}  // namespace
+
+extern "C" void load_config(const char *model_dir, Config *cfg) {
+    memset(cfg, 0, sizeof *cfg);
+    JVal root;
+    if (!parse_json_file(std::string(model_dir) + "/config.json", &root)) return;
+    for (const ConfigKey &k : kConfigKeys)
+        if (!read_config_key(root, k, cfg)) return;
+    if (cfg->n_kv_heads <= 0 || cfg->n_heads % cfg->n_kv_heads != 0) {
+        llm_fail("loader: num_attention_heads must be a multiple of num_key_value_heads");
+        return;
+    }
+    read_eos(model_dir, cfg);
+}
+
+// ------------------------------------------------------------------------------------------
+// safetensors: [u64 little-endian header length N][N bytes of JSON header][data section];
+// header entries {"dtype", "shape", "data_offsets": [begin, end]} relative to the data section.
+// ------------------------------------------------------------------------------------------
+
+namespace {
+
+struct MappedFile {
     std::string path;
-    JVal header;
-    char *gpu_data = nullptr;
+    const char *bytes = nullptr;  // the whole file, read-only
+    size_t size = 0;
+    const char *data = nullptr;   // start of the data section
     size_t data_bytes = 0;
 };
 
-// [u64 little-endian header length N][N bytes of JSON][data]; offsets are relative to the data.
-bool load_shard(const std::string &path, Shard *shard) {
-    shard->path = path;
-    int fd = open(path.c_str(), O_RDONLY);
-    if (fd < 0) return llm_fail("loader: cannot open %s", path.c_str());
-    struct stat st;
-    if (fstat(fd, &st) != 0) {
-        close(fd);
-        return llm_fail("loader: cannot stat %s", path.c_str());
-    }
-    const size_t file_size = (size_t)st.st_size;
-    if (file_size < 8) {
-        close(fd);
-        return llm_fail("loader: %s: too small to be a safetensors file", path.c_str());
-    }
-    void *map = mmap(nullptr, file_size, PROT_READ, MAP_PRIVATE, fd, 0);
-    close(fd);
-    if (map == MAP_FAILED) return llm_fail("loader: cannot mmap %s", path.c_str());
-    const char *bytes = (const char *)map;
-    uint64_t header_len;
-    memcpy(&header_len, bytes, 8);
-    bool ok = true;
-    if (header_len > file_size - 8) {
-        ok = llm_fail("loader: %s: bad header length", path.c_str());
-    } else {
-        JsonParser p(bytes + 8, (size_t)header_len);
-        if (!p.parse(&shard->header) || shard->header.type != JVal::OBJ) {
-            ok = llm_fail("loader: %s: cannot parse header", path.c_str());
-        } else {
-            shard->data_bytes = file_size - 8 - header_len;
-            ok = HIP_OK(hipMalloc((void **)&shard->gpu_data, shard->data_bytes ? shard->data_bytes : 16)) &&
-                 HIP_OK(hipMemcpy(shard->gpu_data, bytes + 8 + header_len, shard->data_bytes,
-                                  hipMemcpyHostToDevice));
-        }
-    }
-    munmap(map, file_size);
-    return ok;
-}
+struct Entry {
+    std::string name, dtype;
+    int shard = 0;
+    std::vector<uint64_t> dims;
+    uint64_t begin = 0, end = 0;
+    bool used = false;
+};
 
-struct Loader {
-    std::vector<Shard> shards;
-    Weights *w = nullptr;
-    int max_tensors = 0;
+// Every tensor of every shard, validated when the headers are read.
+struct Manifest {
+    std::vector<MappedFile> files;
+    std::vector<Entry> entries;
+    std::unordered_map<std::string, size_t> index;
 
-    const JVal *lookup(const char *name, const Shard **shard) const {
-        for (const Shard &s : shards) {
-            const JVal *e = s.header.get(name);
-            if (e) {
-                *shard = &s;
-                return e;
-            }
-        }
-        return nullptr;
+    ~Manifest() {
+        for (MappedFile &f : files)
+            if (f.bytes) munmap((void *)f.bytes, f.size);
     }
-
-    const bf16 *find(const char *name, int n_dims, const int *shape) {
-        const Shard *shard = nullptr;
-        const JVal *e = lookup(name, &shard);
-        if (!e) return llm_fail("loader: tensor %s not found", name), nullptr;
-        const JVal *dtype = e->get("dtype");
-        if (!dtype || dtype->type != JVal::STR || dtype->str != "BF16")
-            return llm_fail("loader: %s: dtype is not BF16", name), nullptr;
-        const JVal *dims = e->get("shape");
-        if (!dims || dims->type != JVal::ARR || (int)dims->arr.size() != n_dims)
-            return llm_fail("loader: %s: expected %d dims", name, n_dims), nullptr;
-        size_t numel = 1;
-        for (int d = 0; d < n_dims; d++) {
-            const int got = (int)dims->arr[d].num;
-            if (got != shape[d])
-                return llm_fail("loader: %s: dim %d is %d, config.json implies %d", name, d, got,
-                                shape[d]),
-                       nullptr;
-            numel *= (size_t)shape[d];
-        }
-        const JVal *off = e->get("data_offsets");
-        if (!off || off->type != JVal::ARR || off->arr.size() != 2)
-            return llm_fail("loader: %s: bad data_offsets", name), nullptr;
-        const size_t begin = (size_t)off->arr[0].num, end = (size_t)off->arr[1].num;
-        if (end > shard->data_bytes || end < begin || end - begin != numel * 2)
-            return llm_fail("loader: %s: data_offsets do not match its shape", name), nullptr;
-        if (begin % 16 != 0)
-            return llm_fail("loader: %s: offset %zu is not 16-byte aligned", name, begin), nullptr;
-        if (w->n_tensors == max_tensors)
-            return llm_fail("loader: %s: loaded more tensors than the files contain", name), nullptr;
-        const bf16 *data = (const bf16 *)(shard->gpu_data + begin);
-        TensorRef *ref = &w->tensors[w->n_tensors++];
-        snprintf(ref->name, sizeof ref->name, "%s", name);
-        ref->data = data;
-        ref->numel = numel;
-        return data;
+    const Entry *find(const std::string &name) const {
+        auto it = index.find(name);
+        return it == index.end() ? nullptr : &entries[it->second];
     }
 };
 
-bool ends_with(const std::string &s, const char *suffix) {
-    size_t n = strlen(suffix);
-    return s.size() >= n && s.compare(s.size() - n, n, suffix) == 0;
+bool map_file(const std::string &path, MappedFile *f) {
+    f->path = path;
+    const int fd = open(path.c_str(), O_RDONLY);
+    if (fd < 0) return llm_fail("loader: cannot open %s", path.c_str());
+    struct stat st;
+    const bool stat_ok = fstat(fd, &st) == 0;
+    if (!stat_ok || st.st_size < 8) {
+        close(fd);
+        return stat_ok ? llm_fail("loader: %s: too small to be a safetensors file", path.c_str())
+                       : llm_fail("loader: cannot stat %s", path.c_str());
+    }
+    void *m = mmap(nullptr, (size_t)st.st_size, PROT_READ, MAP_PRIVATE, fd, 0);
+    close(fd);
+    if (m == MAP_FAILED) return llm_fail("loader: cannot mmap %s", path.c_str());
+    f->bytes = (const char *)m;
+    f->size = (size_t)st.st_size;
+    return true;
+}
+
+// One entry of a shard header: every number a non-negative integer, the byte range inside the
+// data section and 16-byte aligned; for BF16, the range holds exactly the shape's elements.
+bool read_entry(const MappedFile &f, int shard, const std::string &name, const JVal &e,
+                Entry *out) {
+    const char *p = f.path.c_str(), *n = name.c_str();
+    const JVal *dtype = e.get("dtype"), *shape = e.get("shape"), *offs = e.get("data_offsets");
+    if (!dtype || dtype->type != JVal::STR)
+        return llm_fail("loader: %s: tensor %s has no dtype", p, n);
+    if (!shape || shape->type != JVal::ARR)
+        return llm_fail("loader: %s: tensor %s has no shape", p, n);
+    if (!offs || offs->type != JVal::ARR || offs->arr.size() != 2)
+        return llm_fail("loader: %s: tensor %s: data_offsets must be [begin, end]", p, n);
+    out->name = name;
+    out->dtype = dtype->str;
+    out->shard = shard;
+    uint64_t numel = 1;
+    for (const JVal &d : shape->arr) {
+        uint64_t v;
+        if (!json_uint(&d, 4294967295.0, &v))
+            return llm_fail("loader: %s: tensor %s: dims must be non-negative integers", p, n);
+        out->dims.push_back(v);
+        numel *= v;
+    }
+    if (!json_uint(&offs->arr[0], 9007199254740992.0, &out->begin) ||
+        !json_uint(&offs->arr[1], 9007199254740992.0, &out->end))
+        return llm_fail("loader: %s: tensor %s: data_offsets must be non-negative integers", p, n);
+    if (out->end < out->begin || out->end > f.data_bytes)
+        return llm_fail("loader: %s: tensor %s: data_offsets [%" PRIu64 ", %" PRIu64
+                        ") outside the %zu-byte data section",
+                        p, n, out->begin, out->end, f.data_bytes);
+    if (out->begin % 16 != 0)
+        return llm_fail("loader: %s: tensor %s: offset %" PRIu64 " is not 16-byte aligned", p, n,
+                        out->begin);
+    if (out->dtype == "BF16" && out->end - out->begin != numel * 2)
+        return llm_fail("loader: %s: tensor %s: %" PRIu64 " bytes for %" PRIu64 " bf16 elements",
+                        p, n, out->end - out->begin, numel);
+    return true;
+}
+
+bool read_shard(MappedFile *f, int shard, Manifest *m) {
+    uint64_t header_len;
+    memcpy(&header_len, f->bytes, 8);
+    if (header_len > f->size - 8) return llm_fail("loader: %s: bad header length", f->path.c_str());
+    JVal header;
+    JsonParser parser(f->bytes + 8, (size_t)header_len);
+    if (!parser.parse(&header) || header.type != JVal::OBJ)
+        return llm_fail("loader: %s: cannot parse header", f->path.c_str());
+    f->data = f->bytes + 8 + header_len;
+    f->data_bytes = f->size - 8 - (size_t)header_len;
+    for (const auto &kv : header.obj) {
+        if (kv.first == "__metadata__") continue;
+        Entry e;
+        if (!read_entry(*f, shard, kv.first, kv.second, &e)) return false;
+        if (m->index.count(e.name))
+            return llm_fail("loader: tensor %s appears in more than one place", e.name.c_str());
+        m->index.emplace(e.name, m->entries.size());
+        m->entries.push_back(std::move(e));
+    }
+    return true;
+}
+
+bool read_manifest(const char *model_dir, Manifest *m) {
+    DIR *dir = opendir(model_dir);
+    if (!dir) return llm_fail("loader: cannot open directory %s", model_dir);
+    std::vector<std::string> names;
+    for (struct dirent *e = readdir(dir); e; e = readdir(dir)) {
+        const size_t len = strlen(e->d_name), ext = strlen(".safetensors");
+        if (len > ext && strcmp(e->d_name + len - ext, ".safetensors") == 0)
+            names.push_back(e->d_name);
+    }
+    closedir(dir);
+    if (names.empty()) return llm_fail("loader: no .safetensors files in %s", model_dir);
+    if (names.size() > MAX_SHARDS)
+        return llm_fail("loader: %zu .safetensors files in %s (at most %d)", names.size(),
+                        model_dir, MAX_SHARDS);
+    std::sort(names.begin(), names.end());
+    m->files.resize(names.size());
+    for (size_t i = 0; i < names.size(); i++)
+        if (!map_file(std::string(model_dir) + "/" + names[i], &m->files[i]) ||
+            !read_shard(&m->files[i], (int)i, m))
+            return false;
+    return true;
+}
+
+// ---- the schema: the tensors the engine reads, generated from the Config
+
+enum Dim { D_NONE, D_H, D_I, D_QD, D_KVD, D_HEAD, D_VOCAB };
+
+struct LayerTensor {
+    const char *suffix;  // after "model.layers.<l>."
+    Dim rows, cols;      // cols D_NONE: a vector of `rows` elements
+    const bf16 *LayerWeights::*slot;
+};
+
+const LayerTensor kLayerTensors[] = {
+    {"input_layernorm.weight", D_H, D_NONE, &LayerWeights::attn_norm},
+    {"self_attn.q_proj.weight", D_QD, D_H, &LayerWeights::wq},
+    {"self_attn.k_proj.weight", D_KVD, D_H, &LayerWeights::wk},
+    {"self_attn.v_proj.weight", D_KVD, D_H, &LayerWeights::wv},
+    {"self_attn.q_norm.weight", D_HEAD, D_NONE, &LayerWeights::q_norm},
+    {"self_attn.k_norm.weight", D_HEAD, D_NONE, &LayerWeights::k_norm},
+    {"self_attn.o_proj.weight", D_H, D_QD, &LayerWeights::wo},
+    {"post_attention_layernorm.weight", D_H, D_NONE, &LayerWeights::mlp_norm},
+    {"mlp.gate_proj.weight", D_I, D_H, &LayerWeights::w_gate},
+    {"mlp.up_proj.weight", D_I, D_H, &LayerWeights::w_up},
+    {"mlp.down_proj.weight", D_H, D_I, &LayerWeights::w_down},
+};
+
+struct Want {
+    std::string name;
+    std::vector<uint64_t> dims;
+    const bf16 **slot;
+    const Entry *entry = nullptr;
+    size_t dev_offset = 0;  // inside the one device allocation
+};
+
+uint64_t dim_size(const Config *c, Dim d) {
+    switch (d) {
+    case D_H: return (uint64_t)c->hidden_size;
+    case D_I: return (uint64_t)c->intermediate_size;
+    case D_QD: return (uint64_t)c->n_heads * c->head_dim;
+    case D_KVD: return (uint64_t)c->n_kv_heads * c->head_dim;
+    case D_HEAD: return (uint64_t)c->head_dim;
+    case D_VOCAB: return (uint64_t)c->vocab_size;
+    default: return 0;
+    }
+}
+
+std::vector<Want> make_schema(const Config *c, Weights *w) {
+    std::vector<Want> s;
+    auto add = [&](std::string name, Dim rows, Dim cols, const bf16 **slot) {
+        Want x;
+        x.name = std::move(name);
+        x.dims.push_back(dim_size(c, rows));
+        if (cols != D_NONE) x.dims.push_back(dim_size(c, cols));
+        x.slot = slot;
+        s.push_back(std::move(x));
+    };
+    add("model.embed_tokens.weight", D_VOCAB, D_H, &w->embed);
+    for (int l = 0; l < c->n_layers; l++)
+        for (const LayerTensor &t : kLayerTensors)
+            add("model.layers." + std::to_string(l) + "." + t.suffix, t.rows, t.cols,
+                &(w->layers[l].*t.slot));
+    add("model.norm.weight", D_H, D_NONE, &w->final_norm);
+    if (!c->tie_word_embeddings) add("lm_head.weight", D_VOCAB, D_H, &w->lm_head);
+    return s;
+}
+
+std::string dims_text(const std::vector<uint64_t> &d) {
+    std::string s = "[";
+    for (size_t i = 0; i < d.size(); i++) s += (i ? ", " : "") + std::to_string(d[i]);
+    return s + "]";
+}
+
+// Each wanted tensor found, BF16, with the Config's shape; then nothing left over but a tied
+// lm_head.
+bool bind(std::vector<Want> &schema, Manifest &m, bool tied) {
+    for (Want &x : schema) {
+        const Entry *e = m.find(x.name);
+        if (!e) return llm_fail("loader: tensor %s not found", x.name.c_str());
+        if (e->dtype != "BF16")
+            return llm_fail("loader: tensor %s is %s, only BF16 is supported", x.name.c_str(),
+                            e->dtype.c_str());
+        if (e->dims != x.dims)
+            return llm_fail("loader: tensor %s has shape %s, config.json implies %s",
+                            x.name.c_str(), dims_text(e->dims).c_str(), dims_text(x.dims).c_str());
+        x.entry = e;
+        m.entries[e - m.entries.data()].used = true;
+    }
+    int unused = 0;
+    const char *first = nullptr;
+    for (const Entry &e : m.entries)
+        if (!e.used && !(tied && e.name == "lm_head.weight")) {
+            if (!first) first = e.name.c_str();
+            unused++;
+        }
+    if (unused)
+        return llm_fail("loader: %d tensor(s) in the checkpoint are not read by the engine "
+                        "(first: %s)",
+                        unused, first);
+    return true;
 }
 
 }  // namespace
@@ -443,112 +620,83 @@ extern "C" void free_weights(Weights *w) {
 
 extern "C" void load_weights(const char *model_dir, const Config *cfg, Weights *w) {
     memset(w, 0, sizeof *w);
-    Loader ld;
-    ld.w = w;
-    DIR *dir = opendir(model_dir);
-    if (!dir) {
-        llm_fail("loader: cannot open directory %s", model_dir);
+    if (cfg->n_layers <= 0) {
+        llm_fail("loader: num_hidden_layers %d must be positive", cfg->n_layers);
         return;
     }
-    std::vector<std::string> files;
-    for (struct dirent *e = readdir(dir); e; e = readdir(dir))
-        if (ends_with(e->d_name, ".safetensors")) files.push_back(e->d_name);
-    closedir(dir);
-    std::sort(files.begin(), files.end());
-    if (files.empty()) {
-        llm_fail("loader: no .safetensors files in %s", model_dir);
+    w->layers = (LayerWeights *)calloc((size_t)cfg->n_layers, sizeof(LayerWeights));
+    if (!w->layers) {
+        llm_fail("loader: out of memory");
         return;
     }
-    if (files.size() > MAX_SHARDS) {
-        llm_fail("loader: more than %d .safetensors files in %s", MAX_SHARDS, model_dir);
+    Manifest m;
+    std::vector<Want> schema = make_schema(cfg, w);
+    if (!read_manifest(model_dir, &m) || !bind(schema, m, cfg->tie_word_embeddings != 0)) {
+        free_weights(w);
         return;
     }
-    ld.shards.resize(files.size());
-    auto release = [&]() {
-        for (Shard &s : ld.shards)
-            if (s.gpu_data) (void)hipFree(s.gpu_data);
-        free(w->tensors);
-        free(w->layers);
-        memset(w, 0, sizeof *w);
-    };
-    for (size_t i = 0; i < files.size(); i++)
-        if (!load_shard(std::string(model_dir) + "/" + files[i], &ld.shards[i])) {
-            release();
+    size_t total = 0;
+    for (Want &x : schema) {
+        x.dev_offset = total;
+        total += ((x.entry->end - x.entry->begin) + 255) & ~(size_t)255;
+    }
+    w->tensors = (TensorRef *)calloc(schema.size(), sizeof(TensorRef));
+    char *base = nullptr;
+    if (!w->tensors) {
+        llm_fail("loader: out of memory");
+        free_weights(w);
+        return;
+    }
+    if (!HIP_OK(hipMalloc((void **)&base, total ? total : 256))) {
+        free_weights(w);
+        return;
+    }
+    w->gpu_buffers[0] = base;
+    w->n_buffers = 1;
+    w->gpu_bytes = total;
+    for (size_t i = 0; i < schema.size(); i++) {
+        const Want &x = schema[i];
+        const Entry &e = *x.entry;
+        const bf16 *dst = (const bf16 *)(base + x.dev_offset);
+        if (!HIP_OK(hipMemcpy((void *)dst, m.files[e.shard].data + e.begin, e.end - e.begin,
+                              hipMemcpyHostToDevice))) {
+            free_weights(w);
             return;
         }
-    int in_files = 0;
-    for (const Shard &s : ld.shards) {
-        in_files += (int)s.header.obj.size();
-        if (s.header.get("__metadata__")) in_files--;
+        *x.slot = dst;
+        TensorRef *t = &w->tensors[i];
+        snprintf(t->name, sizeof t->name, "%s", x.name.c_str());
+        t->data = dst;
+        t->numel = (e.end - e.begin) / 2;
     }
-    w->tensors = (TensorRef *)calloc(in_files > 0 ? in_files : 1, sizeof(TensorRef));
-    w->layers = (LayerWeights *)calloc(cfg->n_layers > 0 ? cfg->n_layers : 1, sizeof(LayerWeights));
-    ld.max_tensors = in_files;
-    const int H = cfg->hidden_size, D = cfg->head_dim, I = cfg->intermediate_size;
-    const int q_dim = cfg->n_heads * D, kv_dim = cfg->n_kv_heads * D;
-    auto vec = [&](const char *name, int n) { return ld.find(name, 1, &n); };
-    auto mat = [&](const char *name, int r, int c) {
-        int shape[2] = {r, c};
-        return ld.find(name, 2, shape);
-    };
-    char name[96];
-    auto lname = [&](int l, const char *suffix) {
-        snprintf(name, sizeof name, "model.layers.%d.%s", l, suffix);
-        return name;
-    };
-    w->embed = mat("model.embed_tokens.weight", cfg->vocab_size, H);
-    for (int l = 0; l < cfg->n_layers && !llm_has_error(); l++) {
-        LayerWeights *L = &w->layers[l];
-        L->attn_norm = vec(lname(l, "input_layernorm.weight"), H);
-        L->wq = mat(lname(l, "self_attn.q_proj.weight"), q_dim, H);
-        L->wk = mat(lname(l, "self_attn.k_proj.weight"), kv_dim, H);
-        L->wv = mat(lname(l, "self_attn.v_proj.weight"), kv_dim, H);
-        L->q_norm = vec(lname(l, "self_attn.q_norm.weight"), D);
-        L->k_norm = vec(lname(l, "self_attn.k_norm.weight"), D);
-        L->wo = mat(lname(l, "self_attn.o_proj.weight"), H, q_dim);
-        L->mlp_norm = vec(lname(l, "post_attention_layernorm.weight"), H);
-        L->w_gate = mat(lname(l, "mlp.gate_proj.weight"), I, H);
-        L->w_up = mat(lname(l, "mlp.up_proj.weight"), I, H);
-        L->w_down = mat(lname(l, "mlp.down_proj.weight"), H, I);
-    }
-    if (!llm_has_error()) w->final_norm = vec("model.norm.weight", H);
-    if (!llm_has_error())
-        w->lm_head = cfg->tie_word_embeddings ? w->embed : mat("lm_head.weight", cfg->vocab_size, H);
-    if (llm_has_error()) {
-        release();
-        return;
-    }
-    const Shard *unused_shard = nullptr;
-    const int allowed = (cfg->tie_word_embeddings && ld.lookup("lm_head.weight", &unused_shard)) ? 1 : 0;
-    const int unused = in_files - w->n_tensors;
-    if (unused != allowed) {
-        llm_fail("loader: %d tensors in the safetensors files are not used by the engine", unused);
-        release();
-        return;
-    }
-    for (size_t i = 0; i < ld.shards.size(); i++) {
-        w->gpu_buffers[i] = ld.shards[i].gpu_data;
-        w->gpu_bytes += ld.shards[i].data_bytes;
-    }
-    w->n_buffers = (int)ld.shards.size();
+    w->n_tensors = (int)schema.size();
+    if (cfg->tie_word_embeddings) w->lm_head = w->embed;
 }
 
-// src/loader.cu:395-419: per tensor, exact uint64 sums of the raw bits (plain and weighted by
-// position + 1), read back from the device.
+// Per tensor (ref/weight_checksums.py's contract, src/loader.cu:395-419 line format):
+// "<name> <numel> <sum of the raw bf16 bits> <sum of bits * (index + 1)> <first value>", the
+// sums exact modulo 2^64. The tensor is read back in bounded pieces.
 extern "C" void print_weight_checksums(const Weights *w) {
+    const size_t PIECE = (size_t)8 << 20;  // elements per read-back
+    std::vector<uint16_t> buf;
     for (int i = 0; i < w->n_tensors; i++) {
         const TensorRef *t = &w->tensors[i];
-        std::vector<uint16_t> bits(t->numel);
-        if (!HIP_OK(hipMemcpy(bits.data(), t->data, t->numel * 2, hipMemcpyDeviceToHost))) return;
         uint64_t sum = 0, weighted = 0;
-        for (size_t j = 0; j < t->numel; j++) {
-            sum += bits[j];
-            weighted += (uint64_t)(j + 1) * bits[j];
+        uint16_t first = 0;
+        for (size_t at = 0; at < t->numel; at += PIECE) {
+            const size_t n = std::min(PIECE, t->numel - at);
+            buf.resize(n);
+            if (!HIP_OK(hipMemcpy(buf.data(), t->data + at, n * 2, hipMemcpyDeviceToHost))) return;
+            if (at == 0) first = buf[0];
+            for (size_t j = 0; j < n; j++) {
+                sum += buf[j];
+                weighted += (uint64_t)(at + j + 1) * buf[j];
+            }
         }
-        uint32_t first_bits = (uint32_t)(t->numel ? bits[0] : 0) << 16;
-        float first;
-        memcpy(&first, &first_bits, 4);
-        printf("%s %zu %" PRIu64 " %" PRIu64 " %.6g\n", t->name, t->numel, sum, weighted, first);
+        uint32_t fbits = (uint32_t)first << 16;
+        float fval;
+        memcpy(&fval, &fbits, 4);
+        printf("%s %zu %" PRIu64 " %" PRIu64 " %.6g\n", t->name, t->numel, sum, weighted, fval);
     }
     fflush(stdout);
 }

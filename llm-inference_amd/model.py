@@ -157,10 +157,13 @@ def copy_to_host(ptr, nbytes, out=None):
     return out
 
 
-def copy_to_device(ptr, arr):
-    """Synchronous host-to-device copy of a contiguous numpy array to device address ptr."""
+def copy_to_device(ptr, arr, capacity):
+    """Synchronous host-to-device copy of a contiguous numpy array to device address ptr, whose
+    allocation holds `capacity` bytes (a larger array is refused before anything is copied)."""
     import numpy as np
     arr = np.ascontiguousarray(arr)
+    if arr.nbytes > capacity:
+        raise LlmError(f"copy_to_device: {arr.nbytes} bytes for a {capacity}-byte destination")
     rt = _hip()
     rc = rt.hipMemcpy(ptr, arr.ctypes.data, arr.nbytes, 1)  # hipMemcpyHostToDevice
     if rc != 0:
@@ -283,7 +286,7 @@ class Decoder:
             a = np.ascontiguousarray(arr, dtype=np.uint16).reshape(-1)
             if a.size != numel:
                 raise LlmError(f"{name}: {a.size} elements for a tensor of {numel}")
-            copy_to_device(ptr, a)
+            copy_to_device(ptr, a, numel * 2)
 
     def host_weights(self):
         """{safetensors name: uint16 numpy array} of every weight (2-D for matrices)."""
@@ -323,9 +326,18 @@ class Decoder:
         return k, v
 
     def set_kv_cache(self, k, v):
-        """Overwrites the device KV caches with uint16 arrays [n_layers, max_seq, kv_dim]."""
-        copy_to_device(self.s.key_cache, k)
-        copy_to_device(self.s.value_cache, v)
+        """Overwrites the device KV caches with uint16 arrays [n_layers, max_seq, kv_dim] (the
+        run state's max_seq; any other shape or dtype is refused)."""
+        import numpy as np
+        c = self.cfg
+        shape = (c.n_layers, self.s.max_seq, c.n_kv_heads * c.head_dim)
+        for name, a in (("k", k), ("v", v)):
+            if a.dtype != np.uint16 or tuple(a.shape) != shape:
+                raise LlmError(f"set_kv_cache: {name} is {a.dtype}{list(a.shape)}, the cache is "
+                               f"uint16{list(shape)}")
+        nbytes = int(np.prod(shape)) * 2
+        copy_to_device(self.s.key_cache, k, nbytes)
+        copy_to_device(self.s.value_cache, v, nbytes)
 
     def weight_bytes_per_step(self):
         return weight_bytes_per_step(self.cfg)

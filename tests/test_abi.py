@@ -184,3 +184,198 @@ def test_load_weights_header_errors(tmp_path):
     L.load_weights(str(d).encode(), ctypes.byref(cfg), ctypes.byref(w))
     assert "no .safetensors files" in L.llm_last_error().decode()
     L.llm_clear_error()
+
+
+# ---------------------------------------------------------------- loader: manifest and schema
+
+def _small_tensors():
+    """{name: (dtype, shape, bytes)} of a complete checkpoint for CFG (zero-filled BF16)."""
+    H, I, D, V = 256, 512, 128, 1000
+    qd, kvd = 4 * D, 2 * D
+    shapes = {"model.embed_tokens.weight": (V, H), "model.norm.weight": (H,)}
+    for l in range(2):
+        p = f"model.layers.{l}."
+        shapes.update({p + "input_layernorm.weight": (H,), p + "self_attn.q_proj.weight": (qd, H),
+                       p + "self_attn.k_proj.weight": (kvd, H),
+                       p + "self_attn.v_proj.weight": (kvd, H),
+                       p + "self_attn.q_norm.weight": (D,), p + "self_attn.k_norm.weight": (D,),
+                       p + "self_attn.o_proj.weight": (H, qd),
+                       p + "post_attention_layernorm.weight": (H,),
+                       p + "mlp.gate_proj.weight": (I, H), p + "mlp.up_proj.weight": (I, H),
+                       p + "mlp.down_proj.weight": (H, I)})
+    out = {}
+    for name, shape in shapes.items():
+        n = 1
+        for s in shape:
+            n *= s
+        out[name] = ("BF16", list(shape), n * 2)
+    return out
+
+
+def _write_checkpoint(path, tensors, patch=None):
+    """One safetensors file; `patch(header)` may edit the header dict before it is written."""
+    header, off = {}, 0
+    for name, (dtype, shape, nbytes) in tensors.items():
+        header[name] = {"dtype": dtype, "shape": shape, "data_offsets": [off, off + nbytes]}
+        off += nbytes + (-nbytes) % 16
+    if patch:
+        patch(header)
+    h = json.dumps(header).encode()
+    h += b" " * ((-len(h)) % 16)
+    path.write_bytes(struct.pack("<Q", len(h)) + h + b"\0" * off)
+
+
+def _load_error(tmp_path, tensors, patch=None, cfg=CFG):
+    pkg = load_package()
+    from llm_inference_amd import model
+    import ctypes
+    d = _model_dir(tmp_path, cfg)
+    for f in d.glob("*.safetensors"):
+        f.unlink()
+    _write_checkpoint(d / "model.safetensors", tensors, patch)
+    c = model.load_config(d)
+    L = pkg.lib()
+    w = model.Weights()
+    L.llm_clear_error()
+    L.load_weights(str(d).encode(), ctypes.byref(c), ctypes.byref(w))
+    msg = L.llm_last_error()
+    L.llm_clear_error()
+    assert w.n_tensors == 0 and w.n_buffers == 0  # nothing kept on failure
+    return msg.decode() if msg else ""
+
+
+def _set(name, key, value):
+    def patch(h):
+        h[name][key] = value
+    return patch
+
+
+@pytest.mark.parametrize("case,message", [
+    ("missing", "tensor model.layers.1.mlp.up_proj.weight not found"),
+    ("dtype", "is F16, only BF16 is supported"),
+    ("shape", "has shape [512, 255], config.json implies [512, 256]"),
+    ("unaligned", "offset 8 is not 16-byte aligned"),
+    ("negative", "data_offsets must be non-negative integers"),
+    ("fraction", "data_offsets must be non-negative integers"),
+    ("string_dim", "dims must be non-negative integers"),
+    ("negative_dim", "dims must be non-negative integers"),
+    ("outside", "outside the"),
+    ("size", "bytes for 131072 bf16 elements"),
+    ("unused", "1 tensor(s) in the checkpoint are not read by the engine (first: extra.weight)"),
+    ("untied_head", "tensor lm_head.weight not found"),
+])
+def test_load_weights_validation_errors(tmp_path, case, message):
+    """Every format and shape rule is checked before any device memory is touched (so these run
+    without a GPU): missing tensors, dtypes other than BF16, shapes config.json does not imply,
+    misaligned, negative, fractional or out-of-range data offsets, malformed dims, byte counts
+    that disagree with the shape, and tensors the engine would not read."""
+    t = _small_tensors()
+    patch, cfg = None, CFG
+    up = "model.layers.1.mlp.up_proj.weight"
+    if case == "missing":
+        del t[up]
+    elif case == "dtype":
+        t[up] = ("F16",) + t[up][1:]
+    elif case == "shape":
+        t[up] = ("BF16", [512, 255], 512 * 255 * 2)
+    elif case == "unaligned":
+        patch = _set("model.norm.weight", "data_offsets", [8, 8 + 512])
+    elif case == "negative":
+        patch = _set("model.norm.weight", "data_offsets", [-16, 496])
+    elif case == "fraction":
+        patch = _set("model.norm.weight", "data_offsets", [0.5, 512])
+    elif case == "string_dim":
+        patch = _set("model.norm.weight", "shape", ["256"])
+    elif case == "negative_dim":
+        patch = _set("model.norm.weight", "shape", [-256])
+    elif case == "outside":
+        patch = _set("model.norm.weight", "data_offsets", [1 << 40, (1 << 40) + 512])
+    elif case == "size":
+        patch = _set(up, "data_offsets", [0, 1000])
+    elif case == "unused":
+        t["extra.weight"] = ("BF16", [8], 16)
+    elif case == "untied_head":
+        cfg = dict(CFG, tie_word_embeddings=False)
+    msg = _load_error(tmp_path, t, patch, cfg)
+    assert message in msg, msg
+
+
+def test_load_weights_duplicate_across_shards(tmp_path):
+    """A tensor name in two shards is an error, whichever shard would be read."""
+    pkg = load_package()
+    from llm_inference_amd import model
+    import ctypes
+    d = _model_dir(tmp_path)
+    t = _small_tensors()
+    _write_checkpoint(d / "a.safetensors", t)
+    _write_checkpoint(d / "b.safetensors", {"model.norm.weight": t["model.norm.weight"]})
+    c = model.load_config(d)
+    L = pkg.lib()
+    w = model.Weights()
+    L.llm_clear_error()
+    L.load_weights(str(d).encode(), ctypes.byref(c), ctypes.byref(w))
+    msg = L.llm_last_error().decode()
+    L.llm_clear_error()
+    assert "tensor model.norm.weight appears in more than one place" in msg
+
+
+def test_load_weights_tied_head_may_be_present(tmp_path):
+    """With tie_word_embeddings an lm_head.weight in the files is allowed (not read): a complete
+    checkpoint passes every check and only then reaches the device (without a GPU the first HIP
+    call reports the error; on a GPU box the load succeeds)."""
+    t = _small_tensors()
+    t["lm_head.weight"] = ("BF16", [1000, 256], 1000 * 256 * 2)
+    msg = _load_error_or_none(tmp_path, t)
+    assert msg is None or msg.startswith("HIP error"), msg
+
+
+def _load_error_or_none(tmp_path, tensors):
+    pkg = load_package()
+    from llm_inference_amd import model
+    import ctypes
+    d = _model_dir(tmp_path)
+    _write_checkpoint(d / "model.safetensors", tensors)
+    c = model.load_config(d)
+    L = pkg.lib()
+    w = model.Weights()
+    L.llm_clear_error()
+    L.load_weights(str(d).encode(), ctypes.byref(c), ctypes.byref(w))
+    msg = L.llm_last_error()
+    L.llm_clear_error()
+    if msg is None:
+        L.free_weights(ctypes.byref(w))
+    return msg.decode() if msg else None
+
+
+def test_load_config_rejects_fractional_sizes(tmp_path):
+    pkg = load_package()
+    from llm_inference_amd import model
+    with pytest.raises(pkg.LlmError, match='"hidden_size" must be a non-negative integer'):
+        model.load_config(_model_dir(tmp_path, dict(CFG, hidden_size=256.5)))
+    with pytest.raises(pkg.LlmError, match='bad "eos_token_id"'):
+        model.load_config(_model_dir(tmp_path, gen={"eos_token_id": [-1]}))
+
+
+# ---------------------------------------------------------------- byte counts
+
+def test_byte_counts_match_the_published_figures():
+    """weight_bytes_per_step and kv_bytes_per_position through the C ABI: the bytes per token
+    at the mean position of a 5-token prompt + 256 tokens (133.5) equal the reference's published
+    counts for Qwen3-0.6B / 1.7B / 4B (bench/results.csv:289, :317, :345), and the 4B line of the
+    8192-position config (mean position 8320.5) equals 9,271,848,960 B."""
+    load_package()
+    from llm_inference_amd import model
+    published = {"0.6B": 1207412736, "1.7B": 3456464896, "4B": 8064626688}
+    for size, want in published.items():
+        c = model.qwen3_config(size)
+        w, kv = model.weight_bytes_per_step(c), model.kv_bytes_per_position(c)
+        assert kv == 2 * c.n_layers * c.n_kv_heads * c.head_dim * 2
+        assert w + kv * 133.5 == want, size
+    c = model.qwen3_config("4B")
+    assert model.weight_bytes_per_step(c) + model.kv_bytes_per_position(c) * 8320.5 == 9271848960
+    # a model with untied-size terms: every weight once, plus one embedding row
+    c = model.make_config(hidden_size=64, intermediate_size=96, n_layers=3, n_heads=4,
+                          n_kv_heads=2, head_dim=16, vocab_size=50)
+    H, I, D, qd, kvd = 64, 96, 16, 64, 32
+    layer = H + qd * H + 2 * kvd * H + 2 * D + H * qd + H + 2 * I * H + H * I
+    assert model.weight_bytes_per_step(c) == 2 * (3 * layer + H + 50 * H + H)

@@ -251,12 +251,16 @@ def _rope_case(rng, n_tokens, hq, hkv, D, max_seq):
 
 @pytest.mark.parametrize("hq,hkv,D,pos", [(16, 8, 128, 0), (16, 8, 128, 1), (16, 8, 128, 3071),
                                           (32, 8, 128, 4095), (4, 2, 64, 77), (4, 2, 256, 500),
-                                          (3, 1, 128, 9)])
+                                          (3, 1, 128, 9), (32, 8, 128, 4096), (32, 8, 128, 8191),
+                                          (32, 8, 128, 8447)])
 def test_qk_norm_rope_decode(gpu, oracle, hq, hkv, D, pos):
-    """Config-1 decode: q/k rotated in place bit-exactly, k'/v written to cache row pos only."""
+    """Config-1 decode: q/k rotated in place bit-exactly, k'/v written to cache row pos only.
+    Positions past the reference's 4096-slot cap (src/forward.cu:7-8) use an 8448-slot cache, the
+    size of the Qwen3-4B 8192-position config: the rows at 4096, 8191 and 8447 are written and
+    every other row keeps its sentinel."""
     ident(f"qk_norm_rope decode {hq}/{hkv} D{D} pos{pos}")
     rng = np.random.default_rng(hq * 1000 + pos)
-    max_seq = 4096
+    max_seq = 4096 if pos < 4096 else 8448
     q, k, v, qn, kn, kc, vc = _rope_case(rng, 1, hq, hkv, D, max_seq)
     qd, kd, kcd, vcd = dev(q), dev(k), dev(kc), dev(vc)
     qt, kt = dev(np.zeros_like(q)), dev(np.zeros_like(k))
@@ -315,6 +319,33 @@ def test_attention(gpu, oracle, hq, hkv, pos):
     kc = rand_bf16(rng, (max_seq, hkv * D))
     vc = rand_bf16(rng, (max_seq, hkv * D))
     import torch
+    att = torch.zeros(gpu.attention_workspace_floats(hq, D, max_seq), dtype=torch.float32,
+                      device="cuda")
+    out = dev(np.zeros(hq * D, np.uint16))
+    scale = float(np.float32(1.0 / np.sqrt(D)))
+    gpu.attention_forward(out, dev(q), dev(kc), dev(vc), att, hq, hkv, D, dev_i32([pos]), max_seq,
+                          scale)
+    y = host(out)
+    assert np.array_equal(y, oracle.attention(q, kc, vc, hq, hkv, D, pos, scale, oracle.GPU_ORDER))
+    assert bf16_ulp_diff(y, oracle.attention(q, kc, vc, hq, hkv, D, pos, scale,
+                                             oracle.EXACT)).max() <= 2
+
+
+@pytest.mark.parametrize("D", [64, 256])
+@pytest.mark.parametrize("rep", [1, 2, 4, 8])
+def test_attention_head_dims(gpu, oracle, D, rep):
+    """The head_dim 64 and 256 instantiations of the split-softmax kernels, for every GQA ratio
+    they are built for, at a position that spans several 64-position blocks and ends inside one:
+    bit-identical to the oracle's GPU order, within 2 bf16 ulps of exact arithmetic."""
+    import torch
+    hkv = 2
+    hq, pos = hkv * rep, 200 + 37 * rep
+    ident(f"attention D{D} rep{rep} pos{pos}")
+    rng = np.random.default_rng(D * 100 + rep)
+    max_seq = 512
+    q = rand_bf16(rng, hq * D)
+    kc = rand_bf16(rng, (max_seq, hkv * D))
+    vc = rand_bf16(rng, (max_seq, hkv * D))
     att = torch.zeros(gpu.attention_workspace_floats(hq, D, max_seq), dtype=torch.float32,
                       device="cuda")
     out = dev(np.zeros(hq * D, np.uint16))

@@ -502,3 +502,110 @@ def test_persistent_step_long_context(qwen06b, oracle):
                               orc.bufs["value_cache"].reshape(v.shape)[:, 5000].reshape(-1))
     finally:
         dec.close()
+
+
+def test_graph_step_4b_after_8192_positions(gpu, oracle):
+    """The Qwen3-4B 8192-position config on the step it runs on (the hipGraph of per-layer
+    kernels): full 4B widths (hidden 2560, 32/8 heads, intermediate 9728, vocab 151936), 2 layers
+    to keep the oracle quick, the KV cache's first 8192 positions filled with N(0, 1). Logits and
+    argmax bit-identical to the oracle's GPU order at positions 8192-8199 (each step's KV rows
+    written past the reference's 4096-slot cap and read back by the next), then a one-call
+    generate_greedy of 8 tokens from 8200 equal to the oracle's."""
+    ident("4B graph step from 8192 positions")
+    from llm_inference_amd import model
+    cfg = model.qwen3_config("4B", n_layers=2, max_seq_len=8448)
+    dec = model.Decoder(cfg, ("synth", 21, 0.02, 0.1))
+    try:
+        rng = np.random.default_rng(8192)
+        kvd = cfg.n_kv_heads * cfg.head_dim
+        k = np.zeros((cfg.n_layers, 8448, kvd), np.uint16)
+        v = np.zeros_like(k)
+        k[:, :8192] = rand_bf16(rng, (cfg.n_layers, 8192, kvd))
+        v[:, :8192] = rand_bf16(rng, (cfg.n_layers, 8192, kvd))
+        dec.set_kv_cache(k, v)
+        w = dec.host_weights()
+        orc = oracle.Model(oracle_cfg(cfg), w, max_seq=8448)
+        del w
+        orc.bufs["key_cache"][:] = k.reshape(-1)
+        orc.bufs["value_cache"][:] = v.reshape(-1)
+        dec.capture_graph("graph")
+        assert not dec.persistent
+        tok = int(rng.integers(0, cfg.vocab_size))
+        for pos in range(8192, 8200):
+            dec.forward(tok, pos)
+            nxt = dec.sample_argmax()
+            ref = orc.forward(tok, pos, oracle.GPU_ORDER)
+            assert np.array_equal(dec.logits(), orc.logits), pos
+            assert nxt == ref, pos
+            tok = nxt
+        kk, vv = dec.kv_cache()
+        ok = orc.bufs["key_cache"].reshape(k.shape)
+        ov = orc.bufs["value_cache"].reshape(v.shape)
+        assert np.array_equal(kk[:, 8192:8200], ok[:, 8192:8200])
+        assert np.array_equal(vv[:, 8192:8200], ov[:, 8192:8200])
+        assert np.array_equal(kk[:, 8200:], k[:, 8200:])  # rows past the position untouched
+        got = dec.generate_greedy(tok, 8200, 8)
+        want = []
+        for i in range(8):
+            tok = orc.forward(tok, 8200 + i, oracle.GPU_ORDER)
+            want.append(tok)
+        assert got == want
+    finally:
+        dec.close()
+
+
+def test_recapture_after_new_weights_drops_old_graphs(gpu, oracle):
+    """capture_graph after the caller swaps in new Weights (a separate allocation): the hipGraph
+    step's generate_greedy must read the new weights, not replay a loop graph captured over the
+    old pointers. The old allocation stays alive until the end, so a stale graph would show up
+    as the old model's tokens, not as a memory fault."""
+    ident("recapture with new weights")
+    import ctypes
+    from llm_inference_amd import lib, model
+    cfg = model.make_config(hidden_size=512, intermediate_size=1024, n_layers=2, n_heads=8,
+                            n_kv_heads=4, vocab_size=3000, max_seq_len=64)
+    dec = model.Decoder(cfg, ("synth", 5, 0.02, 0.1))
+    old = dec.w
+    try:
+        dec.capture_graph("graph")
+        first = dec.generate_greedy(7, 0, 12)
+        new = model.Weights()
+        lib().synth_weights(ctypes.byref(cfg), ctypes.byref(new), 99, 0.02, 0.1)
+        dec.w = new
+        dec.capture_graph("graph")
+        got = dec.generate_greedy(7, 0, 12)
+        orc = oracle.Model(oracle_cfg(cfg), dec.host_weights(), max_seq=64)
+        t, want = 7, []
+        for pos in range(12):
+            t = orc.forward(t, pos, oracle.GPU_ORDER)
+            want.append(t)
+        assert got == want
+        assert got != first
+    finally:
+        dec.close()
+        lib().free_weights(ctypes.byref(old))
+
+
+def test_generate_greedy_while_dumping(gpu, tmp_path):
+    """With dumps open, generate_greedy runs each step eagerly and writes one row per tensor and
+    position, with the same tokens as the captured loop."""
+    ident("generate_greedy with dumps")
+    import ctypes
+    from llm_inference_amd import lib, model
+    cfg = model.make_config(hidden_size=512, intermediate_size=1024, n_layers=2, n_heads=8,
+                            n_kv_heads=4, vocab_size=3000, max_seq_len=64)
+    dec = model.Decoder(cfg, ("synth", 6, 0.02, 0.1))
+    try:
+        dec.capture_graph("graph")
+        want = dec.generate_greedy(11, 0, 6)
+        lib().dump_open(str(tmp_path).encode())
+        try:
+            got = dec.generate_greedy(11, 0, 6)
+        finally:
+            lib().dump_close()
+        assert got == want
+        rows = np.fromfile(tmp_path / "logits.bin", dtype=np.float32)
+        assert rows.size == 6 * cfg.vocab_size
+        assert np.fromfile(tmp_path / "L01.out.bin", dtype=np.float32).size == 6 * cfg.hidden_size
+    finally:
+        dec.close()
