@@ -118,6 +118,17 @@ void rmsnorm_gate_up_forward(bf16 *act, const bf16 *w_gate, const bf16 *w_up, co
 void hbm_stream_probe(void *dst, const void *a, const void *b, size_t n_bytes, int mode,
                       hipStream_t stream);
 
+/* No counterpart in the reference: attention_forward (src/kernels.cuh:22-24) without the `att`
+ * argument, for callers that cannot allocate device memory (code under stream capture, tight
+ * serving loops, harnesses that forbid hipMalloc). It allocates nothing: its workspace is a
+ * library-owned device array of 2^20 floats (4 MiB) per device, so
+ * attention_workspace_floats(n_heads, head_dim, max_seq) must not exceed 1048576 (Qwen3-4B's 32
+ * heads of 128 fit up to 10798 positions); larger sizes are an error and nothing is launched.
+ * Every call on a device shares that device's array: calls that overlap on one device race. */
+void attention_forward_noalloc(bf16 *out, const bf16 *q, const bf16 *key_cache,
+                               const bf16 *value_cache, int n_heads, int n_kv_heads, int head_dim,
+                               const int *d_pos, int max_seq, float scale, hipStream_t stream);
+
 /* Floats attention_forward needs in `att` for these sizes. */
 size_t attention_workspace_floats(int n_heads, int head_dim, int max_seq);
 

@@ -22,7 +22,7 @@ __all__ = [
     "qk_norm_rope_rows", "attention_forward", "argmax_forward", "swiglu_forward",
     "attention_workspace_floats", "rmsnorm_qkv_forward", "rmsnorm_gemv_forward",
     "rmsnorm_gate_up_forward", "hbm_stream_probe", "sample_forward", "dump_open",
-    "dump_close", "dump_enabled", "EXPORTED_SYMBOLS",
+    "dump_close", "dump_enabled", "attention_forward_noalloc", "EXPORTED_SYMBOLS",
 ]
 
 # Every symbol include/llm_amd/*.h declares.
@@ -36,7 +36,7 @@ EXPORTED_SYMBOLS = [
     "load_config", "load_weights", "free_weights", "print_weight_checksums",
     "alloc_run_state", "free_run_state", "capture_graph", "forward", "sample_argmax",
     "weight_bytes_per_step", "kv_bytes_per_position", "alloc_run_state_seq", "synth_weights",
-    "synth_fill", "generate_greedy",
+    "synth_fill", "generate_greedy", "attention_forward_noalloc",
 ]
 
 
@@ -61,6 +61,7 @@ _SIGS = {
     "qk_norm_rope_forward": (None, [_vp] * 8 + [_i, _i, _i, _f, _f, _vp, _vp, _vp]),
     "qk_norm_rope_rows": (None, [_vp] * 8 + [_i, _i, _i, _i, _f, _f, _vp, _vp, _vp]),
     "attention_forward": (None, [_vp] * 5 + [_i, _i, _i, _vp, _i, _f, _vp]),
+    "attention_forward_noalloc": (None, [_vp] * 4 + [_i, _i, _i, _vp, _i, _f, _vp]),
     "argmax_forward": (None, [_vp, _vp, _i, _vp]),
     "swiglu_forward": (None, [_vp, _vp, _vp, _sz, _vp]),
     "attention_workspace_floats": (_sz, [_i, _i, _i]),
@@ -226,6 +227,14 @@ def attention_forward(out, q, key_cache, value_cache, att, n_heads, n_kv_heads, 
     _call(lib().attention_forward, _bf16(out, "out"), _bf16(q, "q"),
           _bf16(key_cache, "key_cache"), _bf16(value_cache, "value_cache"), _ptr(att), n_heads,
           n_kv_heads, head_dim, _ptr(d_pos), max_seq, scale, _stream(stream))
+
+
+def attention_forward_noalloc(out, q, key_cache, value_cache, n_heads, n_kv_heads, head_dim,
+                              d_pos, max_seq, scale, stream=None):
+    """attention_forward with the library's own workspace (allocates nothing)."""
+    _call(lib().attention_forward_noalloc, _bf16(out, "out"), _bf16(q, "q"),
+          _bf16(key_cache, "key_cache"), _bf16(value_cache, "value_cache"), n_heads, n_kv_heads,
+          head_dim, _ptr(d_pos), max_seq, scale, _stream(stream))
 
 
 def hbm_stream_probe(dst, a, b, n_bytes, mode, stream=None):

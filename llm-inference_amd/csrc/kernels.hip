@@ -1269,6 +1269,57 @@ extern "C" void attention_forward(bf16 *out, const bf16 *q, const bf16 *key_cach
 #undef ATT
 }
 
+// Workspace of attention_forward_noalloc: a library-owned device array instead of the caller's
+// `att`, for callers that cannot allocate. Each device holds its own copy until the process
+// ends; it keeps the last call's scores, statistics and partial outputs (every value a call
+// reads was written earlier in the same call, so nothing needs clearing). Calls that overlap on
+// one device race on it.
+constexpr size_t ATTN_SCRATCH_FLOATS = (size_t)1 << 20;  // 4 MiB
+static __device__ __align__(256) float scratch[ATTN_SCRATCH_FLOATS];
+
+// The device address of this device's copy of `scratch`, looked up once per device with that
+// device current. In host code the array's name is only a host-side stand-in, never passed to a
+// kernel.
+static float *scratch_on_current_device() {
+    static std::mutex mu;
+    static float *addr[64];
+    int dev = 0;
+    if (!HIP_OK(hipGetDevice(&dev))) return nullptr;
+    if (dev < 0 || dev >= 64) {
+        llm_fail("attention_forward_noalloc: device %d out of range", dev);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        float *p = nullptr;
+        if (!HIP_OK(hipGetSymbolAddress((void **)&p, HIP_SYMBOL(scratch)))) return nullptr;
+        addr[dev] = p;
+    }
+    return addr[dev];
+}
+
+extern "C" void attention_forward_noalloc(bf16 *out, const bf16 *q, const bf16 *key_cache,
+                                          const bf16 *value_cache, int n_heads, int n_kv_heads,
+                                          int head_dim, const int *d_pos, int max_seq,
+                                          float scale, hipStream_t stream) {
+    if (n_heads <= 0 || head_dim <= 0 || max_seq <= 0) {
+        llm_fail("attention_forward_noalloc: n_heads %d, head_dim %d and max_seq %d must be "
+                 "positive", n_heads, head_dim, max_seq);
+        return;
+    }
+    const size_t need = attention_workspace_floats(n_heads, head_dim, max_seq);
+    if (need > ATTN_SCRATCH_FLOATS) {
+        llm_fail("attention_forward_noalloc: %zu floats of workspace for %d heads of %d over %d "
+                 "positions; the library's scratch holds %zu",
+                 need, n_heads, head_dim, max_seq, ATTN_SCRATCH_FLOATS);
+        return;
+    }
+    float *ws = scratch_on_current_device();
+    if (!ws) return;
+    attention_forward(out, q, key_cache, value_cache, ws, n_heads, n_kv_heads, head_dim, d_pos,
+                      max_seq, scale, stream);
+}
+
 // ------------------------------------------------------------------------------------------
 // temperature sampling (src/kernels.cu:546-597)
 // ------------------------------------------------------------------------------------------
