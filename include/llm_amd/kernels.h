@@ -118,6 +118,14 @@ void rmsnorm_gate_up_forward(bf16 *act, const bf16 *w_gate, const bf16 *w_up, co
 void hbm_stream_probe(void *dst, const void *a, const void *b, size_t n_bytes, int mode,
                       hipStream_t stream);
 
+/* Measurement helper: the device read peak, as the reference measures it beside every bench run
+ * (bench/bandwidth.cu:25-116 read_kernel: a grid-stride read over 512 MiB, the best of several
+ * launch shapes). Reads n_bytes of a (n_bytes % 16 == 0, 16-byte aligned) with `blocks`
+ * workgroups of `threads` threads (64..1024, a power of two); *out is written only in the
+ * unlikely case the xor of a thread's data equals 0x9e3779b9. */
+void hbm_read_peak_probe(unsigned *out, const void *a, size_t n_bytes, int blocks, int threads,
+                         hipStream_t stream);
+
 /* No counterpart in the reference: attention_forward (src/kernels.cuh:22-24) without the `att`
  * argument, for callers that cannot allocate device memory (code under stream capture, tight
  * serving loops, harnesses that forbid hipMalloc). It allocates nothing: its workspace is a

@@ -21,7 +21,8 @@ __all__ = [
     "gemv_residual_forward", "qkv_forward", "gate_up_forward", "qk_norm_rope_forward",
     "qk_norm_rope_rows", "attention_forward", "argmax_forward", "swiglu_forward",
     "attention_workspace_floats", "rmsnorm_qkv_forward", "rmsnorm_gemv_forward",
-    "rmsnorm_gate_up_forward", "hbm_stream_probe", "sample_forward", "dump_open",
+    "rmsnorm_gate_up_forward", "hbm_stream_probe", "hbm_read_peak_probe", "sample_forward",
+    "dump_open",
     "dump_close", "dump_enabled", "attention_forward_noalloc", "EXPORTED_SYMBOLS",
 ]
 
@@ -31,7 +32,8 @@ EXPORTED_SYMBOLS = [
     "qkv_forward", "gate_up_forward", "qk_norm_rope_forward", "attention_forward",
     "argmax_forward", "qk_norm_rope_rows", "swiglu_forward", "attention_workspace_floats",
     "rmsnorm_qkv_forward", "rmsnorm_gemv_forward", "rmsnorm_gate_up_forward",
-    "hbm_stream_probe", "sample_forward", "sample_temperature", "dump_open", "dump_close",
+    "hbm_stream_probe", "hbm_read_peak_probe", "sample_forward", "sample_temperature",
+    "dump_open", "dump_close",
     "dump_enabled", "dump_bf16", "dump_f32", "llm_set_exit_on_error", "llm_last_error", "llm_clear_error",
     "load_config", "load_weights", "free_weights", "print_weight_checksums",
     "alloc_run_state", "free_run_state", "capture_graph", "forward", "sample_argmax",
@@ -69,6 +71,7 @@ _SIGS = {
     "rmsnorm_gemv_forward": (None, [_vp] * 4 + [_f, _i, _i, _vp]),
     "rmsnorm_gate_up_forward": (None, [_vp] * 5 + [_f, _i, _i, _vp]),
     "hbm_stream_probe": (None, [_vp, _vp, _vp, _sz, _i, _vp]),
+    "hbm_read_peak_probe": (None, [_vp, _vp, _sz, _i, _i, _vp]),
     "sample_forward": (None, [_vp, _vp, _i, _f, _f, _vp]),
     "dump_open": (None, [ctypes.c_char_p]),
     "dump_close": (None, []),
@@ -242,6 +245,13 @@ def hbm_stream_probe(dst, a, b, n_bytes, mode, stream=None):
     if not isinstance(dst, int) and dst.numel() * dst.element_size() < need:
         raise LlmError(f"dst holds {dst.numel() * dst.element_size()} bytes, the probe needs {need}")
     _call(lib().hbm_stream_probe, _ptr(dst), _ptr(a), _ptr(b), n_bytes, mode, _stream(stream))
+
+
+def hbm_read_peak_probe(out, a, n_bytes, blocks, threads, stream=None):
+    """Reads n_bytes of `a` with `blocks` workgroups of `threads` threads (the read-peak probe);
+    `out` is a device word written only if a thread's xor equals 0x9e3779b9."""
+    _call(lib().hbm_read_peak_probe, _ptr(out), _ptr(a), n_bytes, blocks, threads,
+          _stream(stream))
 
 
 def sample_forward(out, x, n, inv_temp, u, stream=None):

@@ -1440,6 +1440,42 @@ extern "C" void hbm_stream_probe(void *dst, const void *a, const void *b, size_t
     LAUNCH_OK();
 }
 
+// The device's read peak: a grid-stride read of n16 chunks with four non-temporal 16-byte loads
+// in flight per thread, any launch shape. The xor of what a thread read is stored only if it
+// equals a constant no random buffer is expected to produce, so the loads stay live without a
+// write stream.
+__global__ __launch_bounds__(1024) void read_peak_kernel(const u32x4 *a, size_t n16,
+                                                         uint32_t *out) {
+    const size_t threads = (size_t)gridDim.x * blockDim.x;
+    uint32_t acc = 0;
+    for (size_t base = (size_t)blockIdx.x * blockDim.x + threadIdx.x; base < n16;
+         base += 4 * threads) {
+        u32x4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const size_t i = base + u * threads;
+            v[u] = i < n16 ? __builtin_nontemporal_load(a + i) : u32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    if (acc == 0x9e3779b9u) *out = acc;
+}
+
+extern "C" void hbm_read_peak_probe(unsigned *out, const void *a, size_t n_bytes, int blocks,
+                                    int threads, hipStream_t stream) {
+    if (n_bytes % 16 != 0 || !aligned16(a) || out == nullptr || blocks < 1 ||
+        blocks > (1 << 20) || (threads != 64 && threads != 128 && threads != 256 &&
+                               threads != 512 && threads != 1024)) {
+        llm_fail("hbm_read_peak_probe: %zu bytes (a multiple of 16, 16-byte aligned), %d blocks "
+                 "of %d threads (64..1024, a power of two)", n_bytes, blocks, threads);
+        return;
+    }
+    if (n_bytes == 0) return;
+    read_peak_kernel<<<blocks, threads, 0, stream>>>((const u32x4 *)a, n_bytes / 16, out);
+    LAUNCH_OK();
+}
+
 // ------------------------------------------------------------------------------------------
 // argmax (src/kernels.cu:499-544), two stages
 // ------------------------------------------------------------------------------------------

@@ -383,6 +383,31 @@ def test_hbm_stream_probe(gpu):
     assert np.array_equal(out.cpu().numpy().astype(np.uint32), expect)
 
 
+def test_hbm_read_peak_probe(gpu):
+    """The read-peak probe reads every chunk of its grid-stride walk: a buffer of zeros with the
+    magic word in one chunk of a late iteration (thread 5, third pass, fourth load) makes exactly
+    that thread store it; without it nothing is stored. Bad launch shapes are refused."""
+    import torch
+    ident("hbm_read_peak_probe")
+    magic = 0x9e3779b9 - (1 << 32)  # as int32
+    for blocks, threads in [(3, 256), (2, 1024), (7, 64)]:
+        T = blocks * threads
+        n16 = 4 * T * 3 + 7
+        a = torch.zeros(n16 * 4, dtype=torch.int32, device="cuda")
+        out = torch.zeros(1, dtype=torch.int32, device="cuda")
+        gpu.hbm_read_peak_probe(out, a, n16 * 16, blocks, threads)
+        torch.cuda.synchronize()
+        assert int(out.item()) == 0
+        a[4 * (4 * T * 2 + 3 * T + 5)] = magic
+        gpu.hbm_read_peak_probe(out, a, n16 * 16, blocks, threads)
+        torch.cuda.synchronize()
+        assert int(out.item()) == magic
+    with pytest.raises(gpu.LlmError):
+        gpu.hbm_read_peak_probe(out, a, 64, 4, 100)
+    with pytest.raises(gpu.LlmError):
+        gpu.hbm_read_peak_probe(out, a, 24, 4, 256)
+
+
 # ---------------------------------------------------------------- temperature sampling
 
 def test_sample_forward(gpu, oracle):
