@@ -119,7 +119,18 @@ typedef struct {
                                for the q/k/v, o, gate/up and down rows, then for the LM head,
                                and the end; then, for layer 1 and every workgroup, 8 stamps:
                                input staged / results stored for each of its 4 phases */
+    int attn_mode;          /* how the graph and eager steps run QK-norm + RoPE + attention (set
+                               before capture_graph): ATTN_AUTO, ATTN_SEPARATE
+                               (qk_norm_rope_forward + attention_forward) or ATTN_IN_SCORES
+                               (qk_norm_rope_attention_forward) */
 } RunState;
+
+/* RunState::attn_mode. ATTN_AUTO takes ATTN_IN_SCORES when the longest history (max_seq) has
+ * at most 256 (64-position block, kv head) items: every item then recomputes the query heads'
+ * QK-norm + RoPE cheaply (Qwen3-0.6B graph step, 269 positions: +3% tokens/s), while at 8448
+ * positions the 1056 items' redundant rotations cost more than the launch they save (Qwen3-4B:
+ * -2.6%). */
+enum { ATTN_AUTO = 0, ATTN_SEPARATE = 1, ATTN_IN_SCORES = 2 };
 
 /* How capture_graph prepares the step. STEP_AUTO: the persistent step kernel (one cooperative
  * launch per forward; generate_greedy runs all its tokens in one launch) when the shapes have a

@@ -111,6 +111,18 @@ void rmsnorm_gate_up_forward(bf16 *act, const bf16 *w_gate, const bf16 *w_up, co
                              const bf16 *norm_w, float eps, int rows, int cols,
                              hipStream_t stream);
 
+/* No counterpart in the reference: qk_norm_rope_forward followed by attention_forward
+ * (src/kernels.cuh:18-24) for one decode position, with the same bits, in three launches
+ * instead of four: the per-head QK-norm + RoPE is computed inside the attention's scores pass,
+ * per block of positions, while the block's keys stream. q and k are read, not rewritten; k'
+ * and v are written to the caches' row *d_pos as qk_norm_rope_forward writes them. `att`, the
+ * shapes and alignment are attention_forward's. */
+void qk_norm_rope_attention_forward(bf16 *out, const bf16 *q, const bf16 *k, const bf16 *v,
+                                    const bf16 *q_norm_w, const bf16 *k_norm_w, bf16 *key_cache,
+                                    bf16 *value_cache, float *att, const int *d_pos, int n_heads,
+                                    int n_kv_heads, int head_dim, float eps, float theta,
+                                    int max_seq, float scale, hipStream_t stream);
+
 /* Measurement helper, no counterpart in the reference: the streaming ceiling that the
  * bandwidth-bound kernels are compared with. mode 0: read n_bytes of a (dst receives one 32-bit
  * word per thread: at least 1 MiB); mode 1: copy n_bytes from a to dst; mode 2: dst = a ^ b over

@@ -22,7 +22,7 @@ __all__ = [
     "qk_norm_rope_rows", "attention_forward", "argmax_forward", "swiglu_forward",
     "attention_workspace_floats", "rmsnorm_qkv_forward", "rmsnorm_gemv_forward",
     "rmsnorm_gate_up_forward", "hbm_stream_probe", "hbm_read_peak_probe", "sample_forward",
-    "dump_open",
+    "qk_norm_rope_attention_forward", "dump_open",
     "dump_close", "dump_enabled", "attention_forward_noalloc", "EXPORTED_SYMBOLS",
 ]
 
@@ -39,6 +39,7 @@ EXPORTED_SYMBOLS = [
     "alloc_run_state", "free_run_state", "capture_graph", "forward", "sample_argmax",
     "weight_bytes_per_step", "kv_bytes_per_position", "alloc_run_state_seq", "synth_weights",
     "synth_fill", "generate_greedy", "attention_forward_noalloc",
+    "qk_norm_rope_attention_forward",
 ]
 
 
@@ -72,6 +73,7 @@ _SIGS = {
     "rmsnorm_gate_up_forward": (None, [_vp] * 5 + [_f, _i, _i, _vp]),
     "hbm_stream_probe": (None, [_vp, _vp, _vp, _sz, _i, _vp]),
     "hbm_read_peak_probe": (None, [_vp, _vp, _sz, _i, _i, _vp]),
+    "qk_norm_rope_attention_forward": (None, [_vp] * 9 + [_vp, _i, _i, _i, _f, _f, _i, _f, _vp]),
     "sample_forward": (None, [_vp, _vp, _i, _f, _f, _vp]),
     "dump_open": (None, [ctypes.c_char_p]),
     "dump_close": (None, []),
@@ -230,6 +232,19 @@ def attention_forward(out, q, key_cache, value_cache, att, n_heads, n_kv_heads, 
     _call(lib().attention_forward, _bf16(out, "out"), _bf16(q, "q"),
           _bf16(key_cache, "key_cache"), _bf16(value_cache, "value_cache"), _ptr(att), n_heads,
           n_kv_heads, head_dim, _ptr(d_pos), max_seq, scale, _stream(stream))
+
+
+def qk_norm_rope_attention_forward(out, q, k, v, q_norm_w, k_norm_w, key_cache, value_cache, att,
+                                   d_pos, n_heads, n_kv_heads, head_dim, eps, theta, max_seq,
+                                   scale, stream=None):
+    """qk_norm_rope_forward + attention_forward, the QK-norm + RoPE inside the scores pass."""
+    need = attention_workspace_floats(n_heads, head_dim, max_seq)
+    if not isinstance(att, int) and att.numel() < need:
+        raise LlmError(f"att holds {att.numel()} floats, attention needs {need}")
+    _call(lib().qk_norm_rope_attention_forward, _bf16(out, "out"), _bf16(q, "q"), _bf16(k, "k"),
+          _bf16(v, "v"), _bf16(q_norm_w, "q_norm_w"), _bf16(k_norm_w, "k_norm_w"),
+          _bf16(key_cache, "key_cache"), _bf16(value_cache, "value_cache"), _ptr(att), _ptr(d_pos),
+          n_heads, n_kv_heads, head_dim, eps, theta, max_seq, scale, _stream(stream))
 
 
 def attention_forward_noalloc(out, q, key_cache, value_cache, n_heads, n_kv_heads, head_dim,

@@ -185,6 +185,25 @@ __device__ __forceinline__ float group_sum_scatter(const float (&v)[B]) {
     return scatter_sum_step<B, 1, N>(v);
 }
 
+// Reduce-scatter of M values per lane over aligned lane groups of N, from xor distance S on:
+// at each step a lane keeps half of its values (the upper half when bit S of its lane index is
+// set) and adds its partner's copies of them, so every total has the pairing of the butterfly
+// sum; `out` receives the M * S / N values left.
+template <int M, int S, int N>
+__device__ __forceinline__ void scatter_keep(const float *v, float *out) {
+    if constexpr (S >= N) {
+#pragma unroll
+        for (int j = 0; j < M; j++) out[j] = v[j];
+    } else {
+        const bool up = (tid_x() & S) != 0;
+        float keep[M / 2];
+#pragma unroll
+        for (int j = 0; j < M / 2; j++)
+            keep[j] = (up ? v[j + M / 2] : v[j]) + xor_lane<S>(up ? v[j] : v[j + M / 2]);
+        scatter_keep<M / 2, 2 * S, N>(keep, out);
+    }
+}
+
 // Larger value wins, equal values keep the lower index; NaN is never taken.
 __device__ __forceinline__ void amax_pair(float &v, int &i, float v2, int i2) {
     if (v2 > v || (v2 == v && i2 < i)) {

@@ -112,6 +112,9 @@ static bool forward_kernels(const Config *cfg, const Weights *w, RunState *s) {
     // fewer) for hidden sizes of up to 8192.
     const bool dumping = dump_enabled() != 0;
     const bool fuse_norm = H <= 8192 && !dumping;
+    const long attn_items = (long)((s->max_seq + 63) / 64) * cfg->n_kv_heads;
+    const bool fuse_attn = !dumping && (s->attn_mode == ATTN_IN_SCORES ||
+                                        (s->attn_mode == ATTN_AUTO && attn_items <= 256));
     bf16 *tap1 = dumping ? s->tap1 : nullptr, *tap2 = dumping ? s->tap2 : nullptr;
     embedding_checked(s->x, w->embed, s->next_token, H, cfg->vocab_size, s->error_flag, st);
     dump_bf16("embed", s->x, H);
@@ -130,15 +133,23 @@ static bool forward_kernels(const Config *cfg, const Weights *w, RunState *s) {
         dump_layer(l, "q_proj", s->q, q_dim);
         dump_layer(l, "k_proj", s->k, kv_dim);
         dump_layer(l, "v_proj", s->v, kv_dim);
-        qk_norm_rope_forward(s->q, s->k, s->v, L->q_norm, L->k_norm, kc, vc, s->pos, cfg->n_heads,
-                             cfg->n_kv_heads, D, cfg->rms_norm_eps, cfg->rope_theta, tap1, tap2,
-                             st);
-        dump_layer(l, "q_norm", tap1, q_dim);
-        dump_layer(l, "k_norm", tap2, kv_dim);
-        dump_layer(l, "q_rope", s->q, q_dim);
-        dump_layer(l, "k_rope", s->k, kv_dim);
-        attention_forward(s->attn_out, s->q, kc, vc, s->att, cfg->n_heads, cfg->n_kv_heads, D,
-                          s->pos, s->max_seq, scale, st);
+        if (fuse_attn) {
+            // QK-norm + RoPE inside the attention's scores pass (same bits, one launch fewer)
+            qk_norm_rope_attention_launch(s->attn_out, s->q, s->k, s->v, L->q_norm, L->k_norm, kc,
+                                          vc, s->att, s->pos, cfg->n_heads, cfg->n_kv_heads, D,
+                                          cfg->rms_norm_eps, cfg->rope_theta, s->max_seq, scale,
+                                          st);
+        } else {
+            qk_norm_rope_forward(s->q, s->k, s->v, L->q_norm, L->k_norm, kc, vc, s->pos,
+                                 cfg->n_heads, cfg->n_kv_heads, D, cfg->rms_norm_eps,
+                                 cfg->rope_theta, tap1, tap2, st);
+            dump_layer(l, "q_norm", tap1, q_dim);
+            dump_layer(l, "k_norm", tap2, kv_dim);
+            dump_layer(l, "q_rope", s->q, q_dim);
+            dump_layer(l, "k_rope", s->k, kv_dim);
+            attention_forward(s->attn_out, s->q, kc, vc, s->att, cfg->n_heads, cfg->n_kv_heads, D,
+                              s->pos, s->max_seq, scale, st);
+        }
         dump_layer(l, "attn_out", s->attn_out, q_dim);
         gemv_residual_forward(s->x, L->wo, s->attn_out, H, q_dim, tap1, st);
         dump_layer(l, "o_proj", tap1, H);
@@ -303,8 +314,8 @@ static bool check_step_error(const Config *cfg, RunState *s) {
     if (err == 0) return true;
     HIP_OK(hipMemset(s->error_flag, 0, 4));
     HIP_OK(hipMemset(s->step_ws, 0, step_workspace_bytes(cfg)));
-    return llm_fail(err == 2 ? "step kernel: a wait for another workgroup's data timed out"
-                             : "step kernel: token or position out of range on the device");
+    return llm_fail(err == 2 ? "step: a wait for another workgroup's data timed out"
+                             : "step: token or position out of range on the device");
 }
 
 // src/forward.cu:196-204

@@ -14,3 +14,10 @@ int argmax_partial_count();
 
 // inv_freq_j = 1 / fp32(pow(theta, fp32(2j / D))) for j < D/2 (D <= 256), cached per (theta, D).
 void rope_inv_freq_table(float theta, int D, float *out);
+
+// qk_norm_rope_attention_forward, reporting whether it launched.
+bool qk_norm_rope_attention_launch(bf16 *out, const bf16 *q, const bf16 *k, const bf16 *v,
+                                   const bf16 *q_norm_w, const bf16 *k_norm_w, bf16 *key_cache,
+                                   bf16 *value_cache, float *att, const int *d_pos, int n_heads,
+                                   int n_kv_heads, int head_dim, float eps, float theta,
+                                   int max_seq, float scale, hipStream_t stream);

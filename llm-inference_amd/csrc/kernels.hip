@@ -889,25 +889,6 @@ extern "C" void qk_norm_rope_rows(bf16 *q, bf16 *k, const bf16 *v, const bf16 *q
 
 constexpr int ATT_B = 64;  // positions per block
 
-// Reduce-scatter of M values per lane over aligned lane groups of N, from xor distance S on:
-// at each step a lane keeps half of its values (the upper half when bit S of its lane index is
-// set) and adds its partner's copies of them, so every total has the pairing of the butterfly
-// sum; `out` receives the M * S / N values left.
-template <int M, int S, int N>
-__device__ __forceinline__ void scatter_keep(const float *v, float *out) {
-    if constexpr (S >= N) {
-#pragma unroll
-        for (int j = 0; j < M; j++) out[j] = v[j];
-    } else {
-        const bool up = (tid_x() & S) != 0;
-        float keep[M / 2];
-#pragma unroll
-        for (int j = 0; j < M / 2; j++)
-            keep[j] = (up ? v[j + M / 2] : v[j]) + xor_lane<S>(up ? v[j] : v[j + M / 2]);
-        scatter_keep<M / 2, 2 * S, N>(keep, out);
-    }
-}
-
 struct AttnArgs {
     bf16 *out;
     const bf16 *q;
@@ -997,6 +978,157 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(AttnArgs a) {
             }
         }
         __syncthreads();
+    }
+}
+
+// Pass 1 with the QK-norm + RoPE of the position folded in (qk_norm_rope_forward followed by
+// attn_scores_kernel, the same bits): an item requests its key history rows (positions < pos)
+// first, then normalises and rotates its kv head's REP query heads (waves 0 .. QWAVES-1, the
+// qk_norm_rope_kernel lane layout) into LDS while they stream; the item of the block holding
+// pos also rotates the key (next wave), which it uses for position pos and writes, with the
+// value row, into the caches' row pos. Every item of a kv head computes the same roped query
+// heads; nothing waits for another workgroup.
+struct AttnRopeArgs {
+    AttnArgs at;
+    const bf16 *k, *v, *qn, *kn;  // at.q is the query before QK-norm + RoPE
+    bf16 *kc_w, *vc_w;            // the caches, writable (row pos)
+    float eps;
+    float inv_freq[128];
+};
+
+// The rope inputs of one wave (the raw head rows and norm weights), requested before the key
+// rows so that they are not behind them (loads complete in order), and the RoPE table.
+template <int D>
+struct RopeIn {
+    u32x4 xa, xb, wa, wb;
+    float cs[RopeShape<D>::NJ], sn[RopeShape<D>::NJ];
+};
+
+// Waves 0 .. QWAVES-1 take the kv head's REP query heads (HPW per wave, the qk_norm_rope_kernel
+// lane layout); wave QWAVES the key head when `key`. Returns whether this wave has rope work.
+template <int D, int REP>
+__device__ __forceinline__ bool rope_request(const AttnRopeArgs &r, int g, int pos, bool key,
+                                             RopeIn<D> &in) {
+    constexpr int LH = D / 16, HPW = 64 / LH, HALF = D / 2;
+    constexpr int QWAVES = (REP + HPW - 1) / HPW;
+    static_assert(QWAVES < 4 && HPW >= 2, "rope waves");
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    if (w > QWAVES || (w == QWAVES && !key)) return false;
+    const int lane = threadIdx.x & 63, hg = lane / LH, L = lane % LH;
+    const bool is_k = w == QWAVES;
+    const int hl0 = is_k ? 0 : w * HPW;
+    const int n_h = is_k ? 1 : min(HPW, REP - hl0);
+    const bf16 *src = is_k ? r.k + (size_t)g * D : r.at.q + ((size_t)g * REP + hl0) * D;
+    // the wave's heads as one wave-uniform buffer: loads past the last head read zeros
+    const __amdgpu_buffer_rsrc_t xr =
+        __builtin_amdgcn_make_buffer_rsrc((void *)src, (short)0, n_h * D * 2, BUFFER_FLAGS);
+    const int oa = hg * D * 2 + 16 * L, ob = oa + 2 * HALF;
+    in.xa = __builtin_amdgcn_raw_buffer_load_b128(xr, oa, 0, 0);
+    in.xb = __builtin_amdgcn_raw_buffer_load_b128(xr, ob, 0, 0);
+    const bf16 *nw = is_k ? r.kn : r.qn;
+    in.wa = ld16(nw + 8 * L);
+    in.wb = ld16(nw + HALF + 8 * L);
+    return true;
+}
+
+// QK-norm + RoPE of the requested heads into q_out / k_out (LDS); the key wave also writes k'
+// and (its next group of lanes) the value row into the caches' row pos.
+template <int D, int REP>
+__device__ __forceinline__ void rope_finish(const AttnRopeArgs &r, int g, int pos,
+                                            const RopeIn<D> &in, u32x4 *q_out, u32x4 *k_out) {
+    constexpr int LH = D / 16, HPW = 64 / LH, HALF = D / 2;
+    constexpr int QWAVES = (REP + HPW - 1) / HPW;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63, hg = lane / LH, L = lane % LH;
+    const bool is_k = w == QWAVES;
+    const int hl0 = is_k ? 0 : w * HPW;
+    const int n_h = is_k ? 1 : min(HPW, REP - hl0);
+    const size_t kv_dim = (size_t)r.at.n_kv_heads * D;
+    u32x4 ya, yb, va, vb;
+    norm_rope<D>(in.xa, in.xb, in.wa, in.wb, r.eps, in.cs, in.sn, L, ya, yb, va, vb);
+    if (hg < n_h) {
+        u32x4 *dst = is_k ? k_out : q_out + (hl0 + hg) * (D / 8);
+        dst[L] = va;
+        dst[HALF / 8 + L] = vb;
+        if (is_k) {
+            bf16 *row = r.kc_w + (size_t)pos * kv_dim + (size_t)g * D;
+            st16(row + 8 * L, va);
+            st16(row + HALF + 8 * L, vb);
+        }
+    } else if (is_k && hg == 1) {  // the next group of lanes copies the value row
+        const bf16 *vsrc = r.v + (size_t)g * D;
+        bf16 *row = r.vc_w + (size_t)pos * kv_dim + (size_t)g * D;
+        st16(row + 8 * L, ld16(vsrc + 8 * L));
+        st16(row + HALF + 8 * L, ld16(vsrc + HALF + 8 * L));
+    }
+}
+
+template <int D, int REP>
+__global__ __launch_bounds__(256) void attn_rope_scores_kernel(AttnRopeArgs r) {
+    constexpr int LP = D / 8, PPW = 64 / LP, PER_WAVE = ATT_B / 4, ITERS = PER_WAVE / PPW;
+    const AttnArgs &a = r.at;
+    __shared__ float sc[REP][ATT_B];
+    __shared__ u32x4 qk_s[(REP + 1) * (D / 8)];  // the roped query heads, then the key
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int G = lane / LP, L = lane % LP;
+    const int pos = *a.d_pos;
+    const int n = pos + 1;
+    const int nb = (n + ATT_B - 1) / ATT_B;
+    const int kv_dim = a.n_kv_heads * D;
+    for (int item = blockIdx.x; item < nb * a.n_kv_heads; item += gridDim.x) {
+        const int b = item / a.n_kv_heads, g = item - b * a.n_kv_heads;
+        const bool last = b == nb - 1;
+        RopeIn<D> in;
+        const bool roper = rope_request<D, REP>(r, g, pos, last, in);
+        u32x4 kv[ITERS];
+#pragma unroll
+        for (int it = 0; it < ITERS; it++) {
+            const int t = b * ATT_B + w * PER_WAVE + it * PPW + G;
+            kv[it] = t < pos ? ld16_nt(a.kc + (size_t)t * kv_dim + g * D + 8 * L) : u32x4{0, 0, 0, 0};
+        }
+        // the table while the rows stream (arithmetic only)
+        if (roper) rope_table<D>(pos, r.inv_freq, in.cs, in.sn);
+        __syncthreads();  // qk_s of the previous item has been read
+        if (roper) rope_finish<D, REP>(r, g, pos, in, qk_s, qk_s + REP * (D / 8));
+        __syncthreads();
+#pragma unroll
+        for (int it = 0; it < ITERS; it++)
+            if (b * ATT_B + w * PER_WAVE + it * PPW + G == pos) kv[it] = qk_s[REP * (D / 8) + L];
+        // the scores of attn_scores_kernel
+        constexpr int NP = ITERS * REP, SL = NP < LP ? NP : LP;
+        float part[NP];
+#pragma unroll
+        for (int it = 0; it < ITERS; it++)
+#pragma unroll
+            for (int q = 0; q < REP; q++) part[it * REP + q] = dot8(qk_s[q * (D / 8) + L], kv[it], 0.0f);
+#pragma unroll
+        for (int s0 = 0; s0 < NP; s0 += SL) {
+            float slice[SL];
+#pragma unroll
+            for (int j = 0; j < SL; j++) slice[j] = part[s0 + j];
+            const float d = group_sum_scatter<LP, SL>(slice);
+            const int j = s0 + scatter_row<SL>(L), it = j / REP, q = j - it * REP;
+            const int slot = w * PER_WAVE + it * PPW + G;
+            const int t = b * ATT_B + slot;
+            const float s = round_bf(round_bf(d) * a.scale);
+            if (L < SL) {
+                sc[q][slot] = s;
+                if (t < n) a.scores[(size_t)(g * REP + q) * a.max_seq + t] = s;
+            }
+        }
+        __syncthreads();
+        for (int q = w; q < REP; q += 4) {
+            const bool v = b * ATT_B + lane < n;
+            const float s = v ? sc[q][lane] : -__builtin_huge_valf();
+            const float m = wave_max(s);
+            const float e = v ? exp_f32(s - m) : 0.0f;
+            const float S = wave_sum(e);
+            if (lane == 0) {
+                float *st = a.stats + ((size_t)(g * REP + q) * a.max_blocks + b) * 2;
+                st[0] = m;
+                st[1] = S;
+            }
+        }
     }
 }
 
@@ -1204,8 +1336,12 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
 }
 
 template <int D, int REP>
-static void launch_attention_t(const AttnArgs &a, int grid, hipStream_t stream) {
-    attn_scores_kernel<D, REP><<<grid, 256, 0, stream>>>(a);
+static void launch_attention_t(const AttnArgs &a, int grid, hipStream_t stream,
+                               const AttnRopeArgs *rope = nullptr) {
+    if (rope)
+        attn_rope_scores_kernel<D, REP><<<grid, 256, 0, stream>>>(*rope);
+    else
+        attn_scores_kernel<D, REP><<<grid, 256, 0, stream>>>(a);
     if (!LAUNCH_OK()) return;
     attn_pv_kernel<D, REP><<<grid, 256, 0, stream>>>(a);
     if (!LAUNCH_OK()) return;
@@ -1296,6 +1432,54 @@ static float *scratch_on_current_device() {
         addr[dev] = p;
     }
     return addr[dev];
+}
+
+bool qk_norm_rope_attention_launch(bf16 *out, const bf16 *q, const bf16 *k, const bf16 *v,
+                                   const bf16 *q_norm_w, const bf16 *k_norm_w, bf16 *key_cache,
+                                   bf16 *value_cache, float *att, const int *d_pos, int n_heads,
+                                   int n_kv_heads, int head_dim, float eps, float theta,
+                                   int max_seq, float scale, hipStream_t stream) {
+    AttnRopeArgs r;
+    memset(&r, 0, sizeof r);
+    int grid = 0;
+    if (!attention_args(r.at, grid, out, q, key_cache, value_cache, att, n_heads, n_kv_heads,
+                        head_dim, d_pos, max_seq, scale))
+        return false;
+    const void *ptrs[] = {k, v, q_norm_w, k_norm_w};
+    for (const void *p : ptrs)
+        if (!p || !aligned16(p))
+            return llm_fail("qk_norm_rope_attention: k, v and the norm weights must be non-null "
+                            "and 16-byte aligned");
+    r.k = k;
+    r.v = v;
+    r.qn = q_norm_w;
+    r.kn = k_norm_w;
+    r.kc_w = key_cache;
+    r.vc_w = value_cache;
+    r.eps = eps;
+    rope_inv_freq_table(theta, head_dim, r.inv_freq);
+    const int rep = n_heads / n_kv_heads;
+#define ATT(D_, R_)                                        \
+    if (head_dim == D_ && rep == R_) {                     \
+        launch_attention_t<D_, R_>(r.at, grid, stream, &r);\
+        return !llm_has_error();                           \
+    }
+    ATT(64, 1) ATT(64, 2) ATT(64, 4) ATT(64, 8) ATT(128, 1) ATT(128, 2) ATT(128, 4) ATT(128, 8)
+    ATT(256, 1) ATT(256, 2) ATT(256, 4) ATT(256, 8)
+#undef ATT
+    return false;
+}
+
+extern "C" void qk_norm_rope_attention_forward(bf16 *out, const bf16 *q, const bf16 *k,
+                                               const bf16 *v, const bf16 *q_norm_w,
+                                               const bf16 *k_norm_w, bf16 *key_cache,
+                                               bf16 *value_cache, float *att, const int *d_pos,
+                                               int n_heads, int n_kv_heads, int head_dim,
+                                               float eps, float theta, int max_seq, float scale,
+                                               hipStream_t stream) {
+    qk_norm_rope_attention_launch(out, q, k, v, q_norm_w, k_norm_w, key_cache, value_cache, att,
+                                  d_pos, n_heads, n_kv_heads, head_dim, eps, theta, max_seq,
+                                  scale, stream);
 }
 
 extern "C" void attention_forward_noalloc(bf16 *out, const bf16 *q, const bf16 *key_cache,

@@ -51,10 +51,12 @@ class RunState(ctypes.Structure):
                 ("argmax_partials", _vp), ("token_out", _vp), ("token_capacity", _i),
                 ("pos_base", _vp), ("error_flag", _vp), ("loop_graph", _vp), ("step_mode", _i),
                 ("persistent", _i), ("step_ws", _vp), ("layers_dev", _vp), ("step_grid", _i),
-                ("next_token_valid", _i), ("step_trace", ctypes.POINTER(ctypes.c_longlong))]
+                ("next_token_valid", _i), ("step_trace", ctypes.POINTER(ctypes.c_longlong)),
+                ("attn_mode", _i)]
 
 
 STEP_MODES = {"auto": 0, "graph": 1, "persistent": 2}
+ATTN_MODES = {"auto": 0, "separate": 1, "in_scores": 2}
 
 
 _PC, _PW, _PS = ctypes.POINTER(Config), ctypes.POINTER(Weights), ctypes.POINTER(RunState)

@@ -358,6 +358,67 @@ def test_attention_head_dims(gpu, oracle, D, rep):
                                              oracle.EXACT)).max() <= 2
 
 
+FUSED_ATTN_CASES = [(16, 8, 128, 0, 4096), (16, 8, 128, 63, 4096), (16, 8, 128, 64, 4096),
+                    (16, 8, 128, 260, 4096), (32, 8, 128, 8192, 8448), (32, 8, 128, 8447, 8448),
+                    (8, 8, 128, 100, 512), (8, 1, 128, 130, 512), (2, 2, 64, 301, 512),
+                    (16, 2, 64, 200, 512), (4, 2, 256, 777, 1024), (16, 2, 256, 150, 512),
+                    (3, 3, 128, 4100, 4200)]
+
+
+@pytest.mark.parametrize("hq,hkv,D,pos,max_seq", FUSED_ATTN_CASES)
+def test_qk_norm_rope_attention_fused(gpu, oracle, hq, hkv, D, pos, max_seq):
+    """qk_norm_rope_attention_forward (QK-norm + RoPE inside the attention's scores pass): the
+    output is bit-identical to the oracle's GPU order of the two steps (QK-norm + RoPE of q and
+    k, k'/v written to row pos, then attention over rows 0..pos), the caches equal the oracle's
+    (row pos written, every other row keeps its value), q and k are not rewritten. Three calls
+    on one workspace: the case, an earlier position with new inputs, then the first position
+    again with new inputs."""
+    import torch
+    ident(f"qk_norm_rope_attention {hq}/{hkv} D{D} pos{pos} max_seq{max_seq}")
+    rng = np.random.default_rng(hq * 7919 + hkv * 31 + D + pos)
+    kc = rand_bf16(rng, (max_seq, hkv * D))
+    vc = rand_bf16(rng, (max_seq, hkv * D))
+    kcd, vcd = dev(kc), dev(vc)
+    att = torch.zeros(gpu.attention_workspace_floats(hq, D, max_seq), dtype=torch.float32,
+                      device="cuda")
+    scale = float(np.float32(1.0 / np.sqrt(D)))
+    qn = rand_bf16(rng, D, 0.1, 1.0)
+    kn = rand_bf16(rng, D, 0.1, 1.0)
+    for p in [pos, pos // 2, pos]:
+        q = rand_bf16(rng, hq * D)
+        k = rand_bf16(rng, hkv * D)
+        v = rand_bf16(rng, hkv * D)
+        qd, kd = dev(q), dev(k)
+        out = dev(np.zeros(hq * D, np.uint16))
+        gpu.qk_norm_rope_attention_forward(out, qd, kd, dev(v), dev(qn), dev(kn), kcd, vcd, att,
+                                           dev_i32([p]), hq, hkv, D, 1e-6, 1e6, max_seq, scale)
+        eq, ek, ekc, evc = oracle.qk_norm_rope_rows(q[None], k[None], v[None], qn, kn, kc, vc, [p],
+                                                    hq, hkv, D, 1e-6, 1e6, oracle.GPU_ORDER)
+        want = oracle.attention(eq.reshape(-1), ekc, evc, hq, hkv, D, p, scale, oracle.GPU_ORDER)
+        got = host(out)
+        assert np.array_equal(got, want), p
+        assert np.array_equal(host(kcd).reshape(kc.shape), ekc), p
+        assert np.array_equal(host(vcd).reshape(vc.shape), evc), p
+        assert np.array_equal(host(qd), q) and np.array_equal(host(kd), k)
+        kc, vc = ekc, evc
+
+
+def test_qk_norm_rope_attention_fused_rejects(gpu):
+    """Shapes the kernels are not built for are refused with a message."""
+    import torch
+    att = torch.zeros(1 << 16, dtype=torch.float32, device="cuda")
+    x = dev(np.zeros(4096, np.uint16))
+    with pytest.raises(gpu.LlmError):  # head_dim 96
+        gpu.qk_norm_rope_attention_forward(x, x, x, x, x, x, x, x, att, dev_i32([0]), 4, 2, 96,
+                                           1e-6, 1e6, 16, 0.1)
+    with pytest.raises(gpu.LlmError):  # 3 query heads per kv head
+        gpu.qk_norm_rope_attention_forward(x, x, x, x, x, x, x, x, att, dev_i32([0]), 6, 2, 128,
+                                           1e-6, 1e6, 16, 0.1)
+    with pytest.raises(gpu.LlmError):  # no norm weights
+        gpu.qk_norm_rope_attention_forward(x, x, x, x, None, None, x, x, att, dev_i32([0]), 4, 2,
+                                           128, 1e-6, 1e6, 16, 0.1)
+
+
 def test_hbm_stream_probe(gpu):
     """The ceiling probe's three modes compute what they claim (copy, xor of two streams, and a
     per-thread xor of the read chunks), including a length that is not a multiple of the grid."""

@@ -504,14 +504,17 @@ def test_persistent_step_long_context(qwen06b, oracle):
         dec.close()
 
 
-def test_graph_step_4b_after_8192_positions(gpu, oracle):
+@pytest.mark.parametrize("attn", ["fused", "unfused"])
+def test_graph_step_4b_after_8192_positions(gpu, oracle, attn):
     """The Qwen3-4B 8192-position config on the step it runs on (the hipGraph of per-layer
     kernels): full 4B widths (hidden 2560, 32/8 heads, intermediate 9728, vocab 151936), 2 layers
     to keep the oracle quick, the KV cache's first 8192 positions filled with N(0, 1). Logits and
     argmax bit-identical to the oracle's GPU order at positions 8192-8199 (each step's KV rows
     written past the reference's 4096-slot cap and read back by the next), then a one-call
-    generate_greedy of 8 tokens from 8200 equal to the oracle's."""
-    ident("4B graph step from 8192 positions")
+    generate_greedy of 8 tokens from 8200 equal to the oracle's. Both attention forms of the
+    step: QK-norm + RoPE inside the attention's scores pass (the default), and
+    qk_norm_rope_forward + attention_forward."""
+    ident(f"4B graph step from 8192 positions, {attn} attention")
     from llm_inference_amd import model
     cfg = model.qwen3_config("4B", n_layers=2, max_seq_len=8448)
     dec = model.Decoder(cfg, ("synth", 21, 0.02, 0.1))
@@ -528,6 +531,7 @@ def test_graph_step_4b_after_8192_positions(gpu, oracle):
         del w
         orc.bufs["key_cache"][:] = k.reshape(-1)
         orc.bufs["value_cache"][:] = v.reshape(-1)
+        dec.s.attn_mode = model.ATTN_MODES["in_scores" if attn == "fused" else "separate"]
         dec.capture_graph("graph")
         assert not dec.persistent
         tok = int(rng.integers(0, cfg.vocab_size))
