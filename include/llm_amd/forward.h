@@ -121,16 +121,19 @@ typedef struct {
                                input staged / results stored for each of its 4 phases */
     int attn_mode;          /* how the graph and eager steps run QK-norm + RoPE + attention (set
                                before capture_graph): ATTN_AUTO, ATTN_SEPARATE
-                               (qk_norm_rope_forward + attention_forward) or ATTN_IN_SCORES
-                               (qk_norm_rope_attention_forward) */
+                               (qk_norm_rope_forward + attention_forward), ATTN_IN_SCORES
+                               (qk_norm_rope_attention_forward) or ATTN_ONE_PASS
+                               (qk_norm_rope_attention_one_pass) */
+    void *attn_one_pass_ws; /* the one-pass attention's workspace (zeroed at allocation; NULL
+                               where the shapes have no one-pass attention) */
 } RunState;
 
-/* RunState::attn_mode. ATTN_AUTO takes ATTN_IN_SCORES when the longest history (max_seq) has
- * at most 256 (64-position block, kv head) items: every item then recomputes the query heads'
- * QK-norm + RoPE cheaply (Qwen3-0.6B graph step, 269 positions: +3% tokens/s), while at 8448
- * positions the 1056 items' redundant rotations cost more than the launch they save (Qwen3-4B:
- * -2.6%). */
-enum { ATTN_AUTO = 0, ATTN_SEPARATE = 1, ATTN_IN_SCORES = 2 };
+/* RunState::attn_mode. ATTN_AUTO takes ATTN_IN_SCORES when the longest history (max_seq) has at
+ * most 256 (64-position block, kv head) items: every item then recomputes the query heads'
+ * QK-norm + RoPE cheaply (Qwen3-0.6B graph step, 269 positions: +3% tokens/s), else
+ * ATTN_SEPARATE (Qwen3-4B at 8448 positions: 418 tokens/s against 407 for ATTN_IN_SCORES and
+ * 412 for ATTN_ONE_PASS). ATTN_ONE_PASS is taken only when asked for. */
+enum { ATTN_AUTO = 0, ATTN_SEPARATE = 1, ATTN_IN_SCORES = 2, ATTN_ONE_PASS = 3 };
 
 /* How capture_graph prepares the step. STEP_AUTO: the persistent step kernel (one cooperative
  * launch per forward; generate_greedy runs all its tokens in one launch) when the shapes have a
@@ -178,7 +181,7 @@ void synth_fill(bf16 *dev, size_t n, uint64_t seed, uint64_t stream_id, float me
 /* Greedy decode entirely on the device: starting from `token` at position `pos`, replays the
  * captured step n_steps times, feeding each argmax back as the next token. The n_steps greedy
  * tokens are copied to out_tokens (host). One host synchronisation at the end. Returns 0, or
- * -1 if a token left the vocabulary. */
+ * -1 (error recorded) if a token left the vocabulary or a device-side wait timed out. */
 int generate_greedy(const Config *cfg, const Weights *w, RunState *s, int token, int pos,
                     int n_steps, int *out_tokens);
 

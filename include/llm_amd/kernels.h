@@ -123,6 +123,29 @@ void qk_norm_rope_attention_forward(bf16 *out, const bf16 *q, const bf16 *k, con
                                     int n_kv_heads, int head_dim, float eps, float theta,
                                     int max_seq, float scale, hipStream_t stream);
 
+/* No counterpart in the reference: qk_norm_rope_forward followed by attention_forward
+ * (src/kernels.cuh:18-24) for one decode position, with the same bits, in ONE launch: a
+ * workgroup per (kv head, 1/ipk of the 64-position blocks), ipk = CUs / n_kv_heads (at most
+ * 64), that hand the split softmax's block statistics and partial outputs to each other as
+ * tagged words in `ws` instead of through kernel boundaries. The workgroups wait for each
+ * other: the grid never exceeds the CU count, no other work may occupy the device's CUs
+ * meanwhile, and every wait is bounded (on timeout *err = 2 and the output is not valid).
+ * ws: attention_one_pass_bytes(n_heads, head_dim, max_seq) bytes, 256-byte aligned, zeroed
+ * once before the first call and then left to these calls (it holds their launch counter);
+ * calls sharing a ws must not overlap. q, k and v are read, k' and v are written to the
+ * caches' row *d_pos. Supported shapes: attention_one_pass_supported(). */
+void qk_norm_rope_attention_one_pass(bf16 *out, const bf16 *q, const bf16 *k, const bf16 *v,
+                                     const bf16 *q_norm_w, const bf16 *k_norm_w,
+                                     bf16 *key_cache, bf16 *value_cache, void *ws, int *err,
+                                     const int *d_pos, int n_heads, int n_kv_heads,
+                                     int head_dim, float eps, float theta, int max_seq,
+                                     float scale, hipStream_t stream);
+/* Bytes of the one-pass attention's workspace for these sizes. */
+size_t attention_one_pass_bytes(int n_heads, int head_dim, int max_seq);
+/* 1 if qk_norm_rope_attention_one_pass supports these sizes on the current device (head_dim
+ * 128, n_heads / n_kv_heads in {1, 2, 4, 8}, at most 32768 positions), else 0. */
+int attention_one_pass_supported(int n_heads, int n_kv_heads, int head_dim, int max_seq);
+
 /* Measurement helper, no counterpart in the reference: the streaming ceiling that the
  * bandwidth-bound kernels are compared with. mode 0: read n_bytes of a (dst receives one 32-bit
  * word per thread: at least 1 MiB); mode 1: copy n_bytes from a to dst; mode 2: dst = a ^ b over

@@ -24,6 +24,7 @@ __all__ = [
     "rmsnorm_gate_up_forward", "hbm_stream_probe", "hbm_read_peak_probe", "sample_forward",
     "qk_norm_rope_attention_forward", "dump_open",
     "dump_close", "dump_enabled", "attention_forward_noalloc", "EXPORTED_SYMBOLS",
+    "qk_norm_rope_attention_one_pass", "attention_one_pass_bytes", "attention_one_pass_supported",
 ]
 
 # Every symbol include/llm_amd/*.h declares.
@@ -39,7 +40,8 @@ EXPORTED_SYMBOLS = [
     "alloc_run_state", "free_run_state", "capture_graph", "forward", "sample_argmax",
     "weight_bytes_per_step", "kv_bytes_per_position", "alloc_run_state_seq", "synth_weights",
     "synth_fill", "generate_greedy", "attention_forward_noalloc",
-    "qk_norm_rope_attention_forward",
+    "qk_norm_rope_attention_forward", "qk_norm_rope_attention_one_pass",
+    "attention_one_pass_bytes", "attention_one_pass_supported",
 ]
 
 
@@ -74,6 +76,9 @@ _SIGS = {
     "hbm_stream_probe": (None, [_vp, _vp, _vp, _sz, _i, _vp]),
     "hbm_read_peak_probe": (None, [_vp, _vp, _sz, _i, _i, _vp]),
     "qk_norm_rope_attention_forward": (None, [_vp] * 9 + [_vp, _i, _i, _i, _f, _f, _i, _f, _vp]),
+    "qk_norm_rope_attention_one_pass": (None, [_vp] * 11 + [_i, _i, _i, _f, _f, _i, _f, _vp]),
+    "attention_one_pass_bytes": (_sz, [_i, _i, _i]),
+    "attention_one_pass_supported": (_i, [_i, _i, _i, _i]),
     "sample_forward": (None, [_vp, _vp, _i, _f, _f, _vp]),
     "dump_open": (None, [ctypes.c_char_p]),
     "dump_close": (None, []),
@@ -245,6 +250,30 @@ def qk_norm_rope_attention_forward(out, q, k, v, q_norm_w, k_norm_w, key_cache, 
           _bf16(v, "v"), _bf16(q_norm_w, "q_norm_w"), _bf16(k_norm_w, "k_norm_w"),
           _bf16(key_cache, "key_cache"), _bf16(value_cache, "value_cache"), _ptr(att), _ptr(d_pos),
           n_heads, n_kv_heads, head_dim, eps, theta, max_seq, scale, _stream(stream))
+
+
+def attention_one_pass_bytes(n_heads, head_dim, max_seq):
+    return lib().attention_one_pass_bytes(n_heads, head_dim, max_seq)
+
+
+def attention_one_pass_supported(n_heads, n_kv_heads, head_dim, max_seq):
+    return bool(lib().attention_one_pass_supported(n_heads, n_kv_heads, head_dim, max_seq))
+
+
+def qk_norm_rope_attention_one_pass(out, q, k, v, q_norm_w, k_norm_w, key_cache, value_cache, ws,
+                                    err, d_pos, n_heads, n_kv_heads, head_dim, eps, theta,
+                                    max_seq, scale, stream=None):
+    """qk_norm_rope_forward + attention_forward in one launch. ws: a zeroed device buffer of
+    attention_one_pass_bytes() bytes kept between calls; err: a device int32 (2 on timeout)."""
+    need = attention_one_pass_bytes(n_heads, head_dim, max_seq)
+    if not isinstance(ws, int) and ws.numel() * ws.element_size() < need:
+        raise LlmError(f"ws holds {ws.numel() * ws.element_size()} bytes, one-pass attention "
+                       f"needs {need}")
+    _call(lib().qk_norm_rope_attention_one_pass, _bf16(out, "out"), _bf16(q, "q"), _bf16(k, "k"),
+          _bf16(v, "v"), _bf16(q_norm_w, "q_norm_w"), _bf16(k_norm_w, "k_norm_w"),
+          _bf16(key_cache, "key_cache"), _bf16(value_cache, "value_cache"), _ptr(ws), _ptr(err),
+          _ptr(d_pos), n_heads, n_kv_heads, head_dim, eps, theta, max_seq, scale,
+          _stream(stream))
 
 
 def attention_forward_noalloc(out, q, key_cache, value_cache, n_heads, n_kv_heads, head_dim,

@@ -49,6 +49,9 @@ extern "C" void alloc_run_state_seq(RunState *s, const Config *cfg, int max_seq)
               dmalloc(&s->argmax_partials, (size_t)argmax_partial_count() * 8) &&
               dmalloc((void **)&s->pos_base, 4) && dmalloc((void **)&s->error_flag, 4) &&
               dmalloc(&s->step_ws, step_workspace_bytes(cfg));
+    if (ok && attention_one_pass_supported(cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, max_seq))
+        ok = dmalloc(&s->attn_one_pass_ws,
+                     attention_one_pass_bytes(cfg->n_heads, cfg->head_dim, max_seq));
     if (!ok) return;
     HIP_OK(hipStreamCreate(&s->stream));
 }
@@ -61,7 +64,8 @@ extern "C" void free_run_state(RunState *s) {
     void *bufs[] = {s->x,  s->xb,     s->q,      s->k,      s->v,          s->attn_out,
                     s->att, s->key_cache, s->value_cache, s->hb, s->tap1, s->tap2,
                     s->logits, s->next_token, s->pos, s->argmax_partials, s->token_out,
-                    s->pos_base, s->error_flag, s->step_ws, s->layers_dev};
+                    s->pos_base, s->error_flag, s->step_ws, s->layers_dev,
+                    s->attn_one_pass_ws};
     for (void *b : bufs)
         if (b) HIP_OK(hipFree(b));
     if (s->graph) HIP_OK(hipGraphExecDestroy(s->graph));
@@ -113,8 +117,12 @@ static bool forward_kernels(const Config *cfg, const Weights *w, RunState *s) {
     const bool dumping = dump_enabled() != 0;
     const bool fuse_norm = H <= 8192 && !dumping;
     const long attn_items = (long)((s->max_seq + 63) / 64) * cfg->n_kv_heads;
-    const bool fuse_attn = !dumping && (s->attn_mode == ATTN_IN_SCORES ||
-                                        (s->attn_mode == ATTN_AUTO && attn_items <= 256));
+    const bool one_pass = !dumping && s->attn_mode == ATTN_ONE_PASS;
+    if (one_pass && !s->attn_one_pass_ws)
+        return llm_fail("forward: no one-pass attention for these shapes");
+    const bool fuse_attn = !dumping && !one_pass &&
+                           (s->attn_mode == ATTN_IN_SCORES ||
+                            (s->attn_mode == ATTN_AUTO && attn_items <= 256));
     bf16 *tap1 = dumping ? s->tap1 : nullptr, *tap2 = dumping ? s->tap2 : nullptr;
     embedding_checked(s->x, w->embed, s->next_token, H, cfg->vocab_size, s->error_flag, st);
     dump_bf16("embed", s->x, H);
@@ -133,7 +141,13 @@ static bool forward_kernels(const Config *cfg, const Weights *w, RunState *s) {
         dump_layer(l, "q_proj", s->q, q_dim);
         dump_layer(l, "k_proj", s->k, kv_dim);
         dump_layer(l, "v_proj", s->v, kv_dim);
-        if (fuse_attn) {
+        if (one_pass) {
+            // QK-norm + RoPE + attention in one launch (same bits)
+            attention_one_pass_launch(s->attn_out, s->q, s->k, s->v, L->q_norm, L->k_norm, kc, vc,
+                                      s->attn_one_pass_ws, s->error_flag, s->pos, cfg->n_heads,
+                                      cfg->n_kv_heads, D, cfg->rms_norm_eps, cfg->rope_theta,
+                                      s->max_seq, scale, st);
+        } else if (fuse_attn) {
             // QK-norm + RoPE inside the attention's scores pass (same bits, one launch fewer)
             qk_norm_rope_attention_launch(s->attn_out, s->q, s->k, s->v, L->q_norm, L->k_norm, kc,
                                           vc, s->att, s->pos, cfg->n_heads, cfg->n_kv_heads, D,
@@ -386,7 +400,7 @@ extern "C" int sample_temperature(const Config *cfg, RunState *s, float temperat
     if (!HIP_OK(hipMemcpyAsync(&token, s->next_token, 4, hipMemcpyDeviceToHost, s->stream)))
         return -1;
     if (!HIP_OK(hipStreamSynchronize(s->stream))) return -1;
-    if (s->persistent && !check_step_error(cfg, s)) return -1;
+    if (!check_step_error(cfg, s)) return -1;
     if (token < 0) {
         llm_fail("sampling found no token (coin %g)", (double)coin);
         return -1;
@@ -400,7 +414,7 @@ extern "C" int sample_argmax(const Config *cfg, RunState *s) {
     if (!HIP_OK(hipMemcpyAsync(&token, s->next_token, 4, hipMemcpyDeviceToHost, s->stream)))
         return -1;
     if (!HIP_OK(hipStreamSynchronize(s->stream))) return -1;
-    if (s->persistent && !check_step_error(cfg, s)) return -1;
+    if (!check_step_error(cfg, s)) return -1;
     return token;
 }
 
@@ -421,15 +435,14 @@ static bool ensure_token_capacity(RunState *s, int n) {
     return true;
 }
 
-// The n tokens of a device loop to the host, and the loop's error flag: 0, or -1.
-static int copy_tokens_out(RunState *s, int n, int *out_tokens) {
-    int err = 0;
+// The n tokens of a device loop to the host, and the loop's error flag (reported and cleared):
+// 0, or -1.
+static int copy_tokens_out(const Config *cfg, RunState *s, int n, int *out_tokens) {
     if (!HIP_OK(hipMemcpyAsync(out_tokens, s->token_out, (size_t)n * 4, hipMemcpyDeviceToHost,
                                s->stream)) ||
-        !HIP_OK(hipMemcpyAsync(&err, s->error_flag, 4, hipMemcpyDeviceToHost, s->stream)) ||
         !HIP_OK(hipStreamSynchronize(s->stream)))
         return -1;
-    return err ? -1 : 0;
+    return check_step_error(cfg, s) ? 0 : -1;
 }
 
 extern "C" int generate_greedy(const Config *cfg, const Weights *w, RunState *s, int token,
@@ -457,7 +470,7 @@ extern "C" int generate_greedy(const Config *cfg, const Weights *w, RunState *s,
             if (!LAUNCH_OK()) return -1;
         }
         s->next_token_valid = 1;
-        return copy_tokens_out(s, n_steps, out_tokens);
+        return copy_tokens_out(cfg, s, n_steps, out_tokens);
     }
     if (s->persistent) {
         if (!ensure_token_capacity(s, n_steps)) return -1;
@@ -485,7 +498,7 @@ extern "C" int generate_greedy(const Config *cfg, const Weights *w, RunState *s,
     for (int i = 0; i < n_steps; i++)
         if (!HIP_OK(hipGraphLaunch(s->loop_graph, s->stream))) return -1;
     s->next_token_valid = 1;
-    return copy_tokens_out(s, n_steps, out_tokens);
+    return copy_tokens_out(cfg, s, n_steps, out_tokens);
 }
 
 // ------------------------------------------------------------------------------------------

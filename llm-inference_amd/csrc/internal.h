@@ -16,6 +16,13 @@ int argmax_partial_count();
 void rope_inv_freq_table(float theta, int D, float *out);
 
 // qk_norm_rope_attention_forward, reporting whether it launched.
+// qk_norm_rope_attention_one_pass, reporting whether it launched.
+bool attention_one_pass_launch(bf16 *out, const bf16 *q, const bf16 *k, const bf16 *v,
+                               const bf16 *q_norm_w, const bf16 *k_norm_w, bf16 *key_cache,
+                               bf16 *value_cache, void *ws, int *err, const int *d_pos,
+                               int n_heads, int n_kv_heads, int head_dim, float eps, float theta,
+                               int max_seq, float scale, hipStream_t stream);
+
 bool qk_norm_rope_attention_launch(bf16 *out, const bf16 *q, const bf16 *k, const bf16 *v,
                                    const bf16 *q_norm_w, const bf16 *k_norm_w, bf16 *key_cache,
                                    bf16 *value_cache, float *att, const int *d_pos, int n_heads,

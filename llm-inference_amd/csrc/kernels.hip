@@ -1004,6 +1004,30 @@ struct RopeIn {
     float cs[RopeShape<D>::NJ], sn[RopeShape<D>::NJ];
 };
 
+// This lane's RoPE frequencies inv_freq[lane + 64 m], m < NJ, picked out of the argument table
+// with scalar loads and selects. Indexed per lane, the table would be read with a vector load,
+// which the compiler places at its use, after the key rows requested before it; the wait for it
+// would then wait for all of those rows.
+template <int D>
+struct LaneFreq {
+    float f[RopeShape<D>::NJ];
+    __device__ float operator[](int j) const { return f[j >> 6]; }  // j = lane + 64 m
+};
+template <int D>
+__device__ __forceinline__ LaneFreq<D> lane_freq(const float (&table)[128]) {
+    constexpr int NJ = RopeShape<D>::NJ, HALF = RopeShape<D>::HALF;
+    const int lane = threadIdx.x & 63;
+    LaneFreq<D> out;
+#pragma unroll
+    for (int m = 0; m < NJ; m++) {
+        float f = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 64 && 64 * m + k < HALF; k++) f = lane == k ? table[64 * m + k] : f;
+        out.f[m] = f;
+    }
+    return out;
+}
+
 // Waves 0 .. QWAVES-1 take the kv head's REP query heads (HPW per wave, the qk_norm_rope_kernel
 // lane layout); wave QWAVES the key head when `key`. Returns whether this wave has rope work.
 template <int D, int REP>
@@ -1080,6 +1104,7 @@ __global__ __launch_bounds__(256) void attn_rope_scores_kernel(AttnRopeArgs r) {
         const bool last = b == nb - 1;
         RopeIn<D> in;
         const bool roper = rope_request<D, REP>(r, g, pos, last, in);
+        const LaneFreq<D> freq = lane_freq<D>(r.inv_freq);
         u32x4 kv[ITERS];
 #pragma unroll
         for (int it = 0; it < ITERS; it++) {
@@ -1087,7 +1112,7 @@ __global__ __launch_bounds__(256) void attn_rope_scores_kernel(AttnRopeArgs r) {
             kv[it] = t < pos ? ld16_nt(a.kc + (size_t)t * kv_dim + g * D + 8 * L) : u32x4{0, 0, 0, 0};
         }
         // the table while the rows stream (arithmetic only)
-        if (roper) rope_table<D>(pos, r.inv_freq, in.cs, in.sn);
+        if (roper) rope_table<D>(pos, freq, in.cs, in.sn);
         __syncthreads();  // qk_s of the previous item has been read
         if (roper) rope_finish<D, REP>(r, g, pos, in, qk_s, qk_s + REP * (D / 8));
         __syncthreads();
@@ -1333,6 +1358,545 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
         }
     }
     if (threadIdx.x < CC) a.out[(size_t)h * D + c0 + threadIdx.x] = (bf16)f2bf(acc);
+}
+
+// ------------------------------------------------------------------------------------------
+// One-pass attention of the step: QK-norm + RoPE, the scores, the split softmax, PV and the
+// combine in ONE launch, with the arithmetic of qk_norm_rope_kernel followed by
+// attn_scores/pv/combine (the same bits; blocks of 64 positions as there). Workgroup (g, i), i
+// < ipk, of kv head g takes the blocks i, i + ipk, i + 2 ipk, ... of the history. The split
+// softmax has two global steps: every block's statistics before any probability, every block's
+// partial output before the combine. They are handoffs between the ipk workgroups of a kv head,
+// as tagged 64-bit words (float bits << 32 | tag, agent-scope atomic stores and loads; the tag
+// names the launch), so the data is its own ready signal: no counter, no fence, no grid
+// barrier. The combine is split by columns: workgroup i adds, in block order, the partials of
+// its columns of the kv head's query heads. Each workgroup counts its launches in a word of
+// its own (one cache line each: the count every wave reads at the start is not one line that
+// the whole grid queues on), so the tag is that count + 1.
+//
+// Workgroups wait for each other, so all must be resident: the grid never exceeds the CU count
+// (one 512-thread workgroup per CU fits), and every wait is bounded (on timeout the error flag
+// is set and the kernel finishes with what it read).
+// ------------------------------------------------------------------------------------------
+
+constexpr int OP_WAVES = 8, OP_THREADS = 64 * OP_WAVES;
+constexpr int OP_PRE = 3;          // rounds (two blocks each) whose K/V rows are requested first
+constexpr int OP_MAXJ = 16;        // blocks of one workgroup (scores and probabilities in LDS)
+constexpr int OP_MAXB = 512;       // blocks of the history (32768 positions)
+constexpr int OP_MAXCPI = 32;      // combine columns of one workgroup
+constexpr int OP_STAGE = 8192;     // floats staged: statistics, or a chunk of combine partials
+constexpr long long OP_SPIN_LIMIT = 1 << 22;
+constexpr int OP_MAXGRID = 1024;   // workgroups (launch counters in the workspace)
+constexpr int OP_CTR_STRIDE = 16;  // 8-byte words between two counters (128 bytes)
+constexpr size_t OP_HEADER = (size_t)OP_MAXGRID * OP_CTR_STRIDE * 8;
+
+struct OnePassArgs {
+    AttnRopeArgs r;                  // r.at.q: the query before QK-norm + RoPE; r.at.out: output
+    unsigned long long *tstats;      // [n_heads, max_blocks, 2] tagged block max, block sum
+    unsigned long long *tpart;       // [n_heads, max_blocks, D] tagged block partial outputs
+    unsigned long long *launches;    // per workgroup (OP_CTR_STRIDE words apart): its launches
+    int *err;                        // set to 2 when a wait times out
+    int ipk;                         // workgroups per kv head
+    int cpi;                         // combine columns per workgroup
+};
+
+__device__ __forceinline__ unsigned long long op_ld(const unsigned long long *p) {
+    return __hip_atomic_load(gptr((unsigned long long *)p), __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void op_st(unsigned long long *p, float v, uint32_t tag) {
+    __hip_atomic_store(gptr(p), ((unsigned long long)__float_as_uint(v) << 32) | tag,
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Polls the tagged words addr(idx), idx = threadIdx.x + OP_THREADS k < total, until every tag
+// is `tag`, and hands each value to put(idx, value). Bounded: on timeout, or once another
+// workgroup has timed out, it sets *err and goes on with what it read.
+template <class Addr, class Put>
+__device__ __forceinline__ void op_poll(int total, uint32_t tag, int *err, Addr addr, Put put) {
+    constexpr int K = 8;
+    for (int base = 0; base < total; base += OP_THREADS * K) {
+        unsigned long long wv[K];
+        long long spins = 0;
+        for (;;) {
+            bool fresh = true;
+#pragma unroll
+            for (int k = 0; k < K; k++) {
+                const int idx = base + (int)threadIdx.x + OP_THREADS * k;
+                wv[k] = idx < total ? op_ld(addr(idx)) : 0ull;
+                fresh &= idx >= total || (uint32_t)wv[k] == tag;
+            }
+            if (fresh) break;
+            if ((++spins & 15) == 0 &&
+                (spins > OP_SPIN_LIMIT ||
+                 __hip_atomic_load(gptr(err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
+                __hip_atomic_store(gptr(err), 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            const int idx = base + (int)threadIdx.x + OP_THREADS * k;
+            if (idx < total) put(idx, __uint_as_float((uint32_t)(wv[k] >> 32)));
+        }
+    }
+}
+
+template <int REP>
+__global__ __launch_bounds__(OP_THREADS) void attn_one_pass_kernel(OnePassArgs o) {
+    constexpr int D = 128, LP = D / 8, PPW = 64 / LP, ITERS = ATT_B / 4 / PPW;
+    static_assert(ITERS == 4, "a wave takes a quarter (16 positions) of a block");
+    constexpr int MAXC = 4;  // chunks of 64 block statistics held in registers
+    const AttnRopeArgs &r = o.r;
+    const AttnArgs &a = r.at;
+    __shared__ u32x4 qk_s[(REP + 1) * (D / 8)];  // the roped query heads, then the key
+    __shared__ float sc[REP][OP_MAXJ][ATT_B];    // scores, then probabilities
+    __shared__ float red[2][4][REP][D];          // PV quarters of a round's two blocks
+    __shared__ float stage[OP_STAGE];            // statistics / a chunk of combine partials
+    __shared__ float gstat[REP][2];              // each head's global max and sum
+    __shared__ unsigned long long launch_s;
+
+    const int lane = threadIdx.x & 63;
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int half = w >> 2, qtr = w & 3;  // block of a round, quarter of the block
+    const int G = lane / LP, L = lane % LP;
+    const int ipk = o.ipk;
+    const int g = blockIdx.x / ipk, i = blockIdx.x - g * ipk;
+    const int pos = *a.d_pos;
+    if (pos < 0 || pos >= a.max_seq) {  // every workgroup reads the same pos: all return
+        if (threadIdx.x == 0) *o.err = 1;
+        return;
+    }
+    const int n = pos + 1;
+    const int nb = (n + ATT_B - 1) / ATT_B;
+    const int nj = nb > i ? (nb - i + ipk - 1) / ipk : 0;  // blocks of this workgroup
+    const bool owner = (pos / ATT_B) % ipk == i;            // holds the block of pos
+    const int row_bytes = a.n_kv_heads * D * 2;
+    auto slot_pos = [&](int j, int it) {  // position of this lane's slot `it` in block j
+        return (i + ipk * j) * ATT_B + qtr * 16 + it * PPW + G;
+    };
+    // The kv head's K and V history as buffers over rows 0..pos-1: a lane's load of a row at or
+    // past pos, or of a block this workgroup does not have (offset past the end), returns zeros
+    // without a memory access. Every load is then unconditional, so each wait below waits
+    // exactly for the rows it needs (loads complete in order).
+    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(a.kc + g * D), (short)0, pos * row_bytes, BUFFER_FLAGS);
+    const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(a.vc + g * D), (short)0, pos * row_bytes, BUFFER_FLAGS);
+    auto off = [&](int j, int it) { return (uint32_t)(slot_pos(j, it) * row_bytes + 16 * L); };
+    auto rows_of = [&](const __amdgpu_buffer_rsrc_t &all, const bf16 *base, int j) {
+        return j < nj ? all : __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, 0,
+                                                                BUFFER_FLAGS);
+    };
+
+    // Every request is unconditional (absent data: empty buffers), issued in the order of use:
+    // the launch counter, the rope inputs (wave 0: the query heads; wave 1 of the workgroup
+    // holding pos: the key head, and the value row for the cache and PV), this lane's RoPE
+    // frequency, then the K and V rows of the first rounds.
+    const unsigned long long launches = op_ld(o.launches + (size_t)blockIdx.x * OP_CTR_STRIDE);
+    constexpr int LH = D / 16, HALF = D / 2;
+    static_assert(REP <= 64 / LH, "a kv head's query heads in one wave");
+    const bool rq_q = w == 0, rq_k = w == 1 && owner;
+    const int hg = lane / LH, Lr = lane % LH;
+    RopeIn<D> in;
+    {
+        const bf16 *src = rq_k ? r.k + (size_t)g * D : a.q + (size_t)g * REP * D;
+        const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)src, (short)0, rq_q ? REP * D * 2 : rq_k ? D * 2 : 0, BUFFER_FLAGS);
+        in.xa = __builtin_amdgcn_raw_buffer_load_b128(xr, hg * D * 2 + 16 * Lr, 0, 0);
+        in.xb = __builtin_amdgcn_raw_buffer_load_b128(xr, hg * D * 2 + 16 * Lr + D, 0, 0);
+        const __amdgpu_buffer_rsrc_t nr = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(rq_k ? r.kn : r.qn), (short)0, rq_q || rq_k ? D * 2 : 0, BUFFER_FLAGS);
+        in.wa = __builtin_amdgcn_raw_buffer_load_b128(nr, 16 * Lr, 0, 0);
+        in.wb = __builtin_amdgcn_raw_buffer_load_b128(nr, 16 * Lr + D, 0, 0);
+    }
+    // the value row of pos: every lane of the workgroup holding pos (PV), lanes L of wave 1's
+    // second head group write it to the cache
+    const __amdgpu_buffer_rsrc_t vrow = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(r.v + (size_t)g * D), (short)0, owner ? D * 2 : 0, BUFFER_FLAGS);
+    const u32x4 vcur = __builtin_amdgcn_raw_buffer_load_b128(vrow, 16 * L, 0, 0);
+    const u32x4 vcp_a = __builtin_amdgcn_raw_buffer_load_b128(vrow, 16 * Lr, 0, 0);
+    const u32x4 vcp_b = __builtin_amdgcn_raw_buffer_load_b128(vrow, 16 * Lr + D, 0, 0);
+    const LaneFreq<D> freq = lane_freq<D>(r.inv_freq);
+    // the small requests stay ahead of the rows (the compiler would otherwise move them after,
+    // and every wait for them would wait for all the rows too)
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 kpre[OP_PRE][ITERS], vpre[OP_PRE][ITERS];
+#pragma unroll
+    for (int rd = 0; rd < OP_PRE; rd++) {
+        const __amdgpu_buffer_rsrc_t kr = rows_of(krs, a.kc, 2 * rd + half);
+#pragma unroll
+        for (int it = 0; it < ITERS; it++)
+            kpre[rd][it] = __builtin_amdgcn_raw_buffer_load_b128(kr, off(2 * rd + half, it), 0,
+                                                                 BUFFER_NT);
+    }
+#pragma unroll
+    for (int rd = 0; rd < OP_PRE; rd++) {
+        const __amdgpu_buffer_rsrc_t vr = rows_of(vrs, a.vc, 2 * rd + half);
+#pragma unroll
+        for (int it = 0; it < ITERS; it++)
+            vpre[rd][it] = __builtin_amdgcn_raw_buffer_load_b128(vr, off(2 * rd + half, it), 0,
+                                                                 BUFFER_NT);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (rq_q || rq_k) rope_table<D>(pos, freq, in.cs, in.sn);  // while the rows stream
+    if (threadIdx.x == 0) launch_s = launches;
+    __syncthreads();
+    const uint32_t tag = (uint32_t)(launch_s % 0xffffffffull) + 1u;
+    // QK-norm + RoPE (qk_norm_rope_kernel lane layout): the roped query heads and key into
+    // LDS; the workgroup holding pos writes k' and v into the caches' row pos
+    if (rq_q || rq_k) {
+        u32x4 ya, yb, va, vb;
+        norm_rope<D>(in.xa, in.xb, in.wa, in.wb, r.eps, in.cs, in.sn, Lr, ya, yb, va, vb);
+        const size_t row = (size_t)pos * a.n_kv_heads * D + (size_t)g * D;
+        if (rq_q && hg < REP) {
+            qk_s[hg * (D / 8) + Lr] = va;
+            qk_s[hg * (D / 8) + HALF / 8 + Lr] = vb;
+        } else if (rq_k && hg == 0) {
+            qk_s[REP * (D / 8) + Lr] = va;
+            qk_s[REP * (D / 8) + HALF / 8 + Lr] = vb;
+            st16(r.kc_w + row + 8 * Lr, va);
+            st16(r.kc_w + row + HALF + 8 * Lr, vb);
+        } else if (rq_k && hg == 1) {
+            st16(r.vc_w + row + 8 * Lr, vcp_a);
+            st16(r.vc_w + row + HALF + 8 * Lr, vcp_b);
+        }
+    }
+    __syncthreads();
+
+    // scores (attn_scores_kernel): block j's quarter qtr, 16 lanes per position
+    auto scores = [&](int j, const u32x4 (&kr)[ITERS]) {
+        const u32x4 kcur = qk_s[REP * (D / 8) + L];
+        u32x4 qv[REP];
+#pragma unroll
+        for (int q = 0; q < REP; q++) qv[q] = qk_s[q * (D / 8) + L];
+        constexpr int NP = ITERS * REP, SL = NP < LP ? NP : LP;
+        float part[NP];
+#pragma unroll
+        for (int it = 0; it < ITERS; it++) {
+            const u32x4 kk = slot_pos(j, it) == pos ? kcur : kr[it];
+#pragma unroll
+            for (int q = 0; q < REP; q++) part[it * REP + q] = dot8(qv[q], kk, 0.0f);
+        }
+#pragma unroll
+        for (int s0 = 0; s0 < NP; s0 += SL) {
+            float slice[SL];
+#pragma unroll
+            for (int u = 0; u < SL; u++) slice[u] = part[s0 + u];
+            const float d = group_sum_scatter<LP, SL>(slice);
+            const int u = s0 + scatter_row<SL>(L), it = u / REP, q = u - it * REP;
+            if (L < SL) sc[q][j][qtr * 16 + it * PPW + G] = round_bf(round_bf(d) * a.scale);
+        }
+    };
+#pragma unroll
+    for (int rd = 0; rd < OP_PRE; rd++)
+        if (2 * rd + half < nj) scores(2 * rd + half, kpre[rd]);
+    for (int j = 2 * OP_PRE + half; j < nj; j += 2) {
+        u32x4 kr[ITERS];
+#pragma unroll
+        for (int it = 0; it < ITERS; it++)
+            kr[it] = __builtin_amdgcn_raw_buffer_load_b128(rows_of(krs, a.kc, j), off(j, it), 0,
+                                                           BUFFER_NT);
+        scores(j, kr);
+    }
+    __syncthreads();
+
+    // block statistics (max, tree sum of exp(s - max)), published tagged; two (head, block)
+    // pairs per wave at a time
+    for (int p0 = w; p0 < REP * nj; p0 += 2 * OP_WAVES) {
+        float s2[2], m2[2], e2[2], S2[2];
+        bool v2[2];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int p = min(p0 + u * OP_WAVES, REP * nj - 1), q = p % REP, j = p / REP;
+            v2[u] = (i + ipk * j) * ATT_B + lane < n;
+            s2[u] = v2[u] ? sc[q][j][lane] : -__builtin_huge_valf();
+        }
+#pragma unroll
+        for (int u = 0; u < 2; u++) m2[u] = wave_max(s2[u]);
+#pragma unroll
+        for (int u = 0; u < 2; u++) e2[u] = v2[u] ? exp_f32(s2[u] - m2[u]) : 0.0f;
+#pragma unroll
+        for (int u = 0; u < 2; u++) S2[u] = wave_sum(e2[u]);
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+            const int p = p0 + u * OP_WAVES;
+            if (p < REP * nj && lane < 2) {
+                const int q = p % REP, j = p / REP, b = i + ipk * j;
+                unsigned long long *st = o.tstats + ((size_t)(g * REP + q) * a.max_blocks + b) * 2;
+                op_st(st + lane, lane == 0 ? m2[u] : S2[u], tag);
+            }
+        }
+    }
+
+    // every block's statistics of the kv head's query heads, then each head's global max and
+    // sum (attn_pv_kernel order: max over all blocks; chunks of 64 blocks summed by the wave
+    // tree, the chunk sums added in order)
+    op_poll(REP * nb * 2, tag, o.err,
+            [&](int idx) {
+                const int q = idx / (2 * nb), rest = idx - q * 2 * nb;
+                return o.tstats + ((size_t)(g * REP + q) * a.max_blocks) * 2 + rest;
+            },
+            [&](int idx, float v) { stage[idx] = v; });
+    __syncthreads();
+    if (w < REP) {
+        const float *st = stage + w * 2 * nb;
+        float M, sum;
+        if (nb <= 64 * MAXC) {
+            // the chunks' terms and wave sums side by side (independent chains)
+            float mv[MAXC], sv[MAXC], cs[MAXC];
+#pragma unroll
+            for (int c = 0; c < MAXC; c++) {
+                const int bi = min(c * 64 + lane, nb - 1);
+                mv[c] = st[2 * bi];
+                sv[c] = st[2 * bi + 1];
+            }
+            float ml = -__builtin_huge_valf();
+#pragma unroll
+            for (int c = 0; c < MAXC; c++) ml = c * 64 + lane < nb ? fmaxf(ml, mv[c]) : ml;
+            M = wave_max(ml);
+#pragma unroll
+            for (int c = 0; c < MAXC; c++)
+                cs[c] = wave_sum(c * 64 + lane < nb ? sv[c] * exp_f32(mv[c] - M) : 0.0f);
+            sum = cs[0];
+#pragma unroll
+            for (int c = 1; c < MAXC; c++) sum = c * 64 < nb ? sum + cs[c] : sum;
+        } else {
+            float ml = -__builtin_huge_valf();
+            for (int c0 = 0; c0 < nb; c0 += 64)
+                if (c0 + lane < nb) ml = fmaxf(ml, st[2 * (c0 + lane)]);
+            M = wave_max(ml);
+            sum = 0.0f;
+            for (int c0 = 0; c0 < nb; c0 += 64) {
+                const int bi = c0 + lane;
+                const float cs =
+                    wave_sum(bi < nb ? st[2 * bi + 1] * exp_f32(st[2 * bi] - M) : 0.0f);
+                sum = c0 == 0 ? cs : sum + cs;
+            }
+        }
+        if (lane == 0) {
+            gstat[w][0] = M;
+            gstat[w][1] = sum;
+        }
+    }
+    __syncthreads();
+
+    // PV (attn_pv_kernel), per round of two blocks: each wave turns the scores of its quarter
+    // into probabilities p = bf16(exp(s - M) / sum) (0 past the history; only this wave reads
+    // them), lane (G, L) accumulates its 4 slots, the position groups meet in the butterfly's
+    // pairing (reduce-scattered), the quarters are added in order 0..3, and each block's partial
+    // output is published tagged
+    auto pv_round = [&](int rd, const u32x4 (&vr)[ITERS]) {
+        const int j = 2 * rd + half;
+        if (j < nj) {
+            const int b = i + ipk * j;
+#pragma unroll
+            for (int u = 0; u < (REP * 16 + 63) / 64; u++) {
+                const int idx = lane + 64 * u, q = idx / 16, sl = qtr * 16 + idx % 16;
+                if (idx < REP * 16) {
+                    const float s = sc[q][j][sl];
+                    sc[q][j][sl] =
+                        b * ATT_B + sl < n ? round_bf(exp_f32(s - gstat[q][0]) / gstat[q][1]) : 0.0f;
+                }
+            }
+            float acc[REP][8];
+#pragma unroll
+            for (int q = 0; q < REP; q++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) acc[q][e] = 0.0f;
+#pragma unroll
+            for (int it = 0; it < ITERS; it++) {
+                const int t = slot_pos(j, it);
+                if (t < n) {
+                    const u32x4 vt = t == pos ? vcur : vr[it];
+#pragma unroll
+                    for (int q = 0; q < REP; q++) {
+                        const float p = sc[q][j][qtr * 16 + it * PPW + G];
+#pragma unroll
+                        for (int e = 0; e < 8; e++) acc[q][e] = fmaf(p, elem(vt, e), acc[q][e]);
+                    }
+                }
+            }
+            constexpr int NV = REP * 8, NG = 64 / LP, KEEP = NV / NG;
+            float flat[NV], kept[KEEP];
+#pragma unroll
+            for (int q = 0; q < REP; q++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) flat[q * 8 + e] = acc[q][e];
+            scatter_keep<NV, LP, 64>(flat, kept);
+            int off0 = 0;
+#pragma unroll
+            for (int k = 0, m = NV; (LP << k) < 64; k++, m >>= 1)
+                if ((lane >> k) & LP) off0 += m / 2;
+#pragma unroll
+            for (int u = 0; u < KEEP; u++) {
+                const int idx = off0 + u, q = idx / 8, e = idx % 8;
+                red[half][qtr][q][8 * L + e] = kept[u];
+            }
+        }
+        __syncthreads();
+        for (int idx = threadIdx.x; idx < 2 * REP * D; idx += OP_THREADS) {
+            const int h2 = idx / (REP * D), rest = idx - h2 * REP * D;
+            const int q = rest / D, d = rest - q * D, jb = 2 * rd + h2;
+            if (jb < nj) {
+                const float v = ((red[h2][0][q][d] + red[h2][1][q][d]) + red[h2][2][q][d]) +
+                                red[h2][3][q][d];
+                const int b = i + ipk * jb;
+                op_st(o.tpart + ((size_t)(g * REP + q) * a.max_blocks + b) * D + d, v, tag);
+            }
+        }
+        __syncthreads();
+    };
+#pragma unroll
+    for (int rd = 0; rd < OP_PRE; rd++)
+        if (2 * rd < nj) pv_round(rd, vpre[rd]);
+    for (int rd = OP_PRE; 2 * rd < nj; rd++) {
+        u32x4 vr[ITERS];
+#pragma unroll
+        for (int it = 0; it < ITERS; it++)
+            vr[it] = __builtin_amdgcn_raw_buffer_load_b128(rows_of(vrs, a.vc, 2 * rd + half),
+                                                           off(2 * rd + half, it), 0, BUFFER_NT);
+        pv_round(rd, vr);
+    }
+
+    // combine (attn_combine_kernel): columns [c0, c1) of the kv head's REP * D, each the
+    // block partials added in block order, staged in chunks of the blocks
+    const int c0 = i * o.cpi, c1 = min(REP * D, c0 + o.cpi), nc = c1 - c0;
+    if (nc > 0) {
+        const int cb = OP_STAGE / nc;  // blocks per chunk
+        float acc = 0.0f;
+        for (int b0 = 0; b0 < nb; b0 += cb) {
+            const int cnt = min(cb, nb - b0);
+            op_poll(cnt * nc, tag, o.err,
+                    [&](int idx) {
+                        const int bb = idx / nc, c = c0 + idx - bb * nc, q = c / D, d = c - q * D;
+                        return o.tpart + ((size_t)(g * REP + q) * a.max_blocks + b0 + bb) * D + d;
+                    },
+                    [&](int idx, float v) { stage[idx] = v; });
+            __syncthreads();
+            if ((int)threadIdx.x < nc) {
+                const int c = threadIdx.x;
+                int j0 = 0;
+                if (b0 == 0) {
+                    acc = stage[c];
+                    j0 = 1;
+                }
+                for (; j0 + 16 <= cnt; j0 += 16) {  // 16 LDS reads in flight, then the adds
+                    float v[16];
+#pragma unroll
+                    for (int u = 0; u < 16; u++) v[u] = stage[(j0 + u) * nc + c];
+#pragma unroll
+                    for (int u = 0; u < 16; u++) acc += v[u];
+                }
+                for (; j0 < cnt; j0++) acc += stage[j0 * nc + c];
+            }
+            __syncthreads();
+        }
+        if ((int)threadIdx.x < nc) {
+            const int c = c0 + threadIdx.x, q = c / D, d = c - q * D;
+            a.out[(size_t)(g * REP + q) * D + d] = (bf16)f2bf(acc);
+        }
+    }
+    if (threadIdx.x == 0)
+        __hip_atomic_store(gptr(o.launches + (size_t)blockIdx.x * OP_CTR_STRIDE), launch_s + 1,
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+extern "C" size_t attention_one_pass_bytes(int n_heads, int head_dim, int max_seq) {
+    const size_t mb = ceil_div((size_t)max_seq, ATT_B);
+    return OP_HEADER + (size_t)n_heads * mb * 2 * 8 + (size_t)n_heads * mb * head_dim * 8;
+}
+
+// The workgroups per kv head of the one-pass attention on this device (0: not supported).
+static int one_pass_ipk(int n_heads, int n_kv_heads, int head_dim, int max_seq) {
+    if (head_dim != 128 || n_kv_heads <= 0 || n_heads % n_kv_heads != 0) return 0;
+    const int rep = n_heads / n_kv_heads;
+    if (rep != 1 && rep != 2 && rep != 4 && rep != 8) return 0;
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 0;
+    int ipk = (cus < OP_MAXGRID ? cus : OP_MAXGRID) / n_kv_heads;
+    if (ipk > 64) ipk = 64;
+    const int max_blocks = (int)ceil_div((size_t)max_seq, ATT_B);
+    if ((size_t)max_seq * n_kv_heads * head_dim * 2 >= ((size_t)1 << 31)) return 0;
+    if (ipk < 1 || max_blocks > OP_MAXB || max_blocks > ipk * OP_MAXJ ||
+        (rep * head_dim + ipk - 1) / ipk > OP_MAXCPI)
+        return 0;
+    return ipk;
+}
+
+extern "C" int attention_one_pass_supported(int n_heads, int n_kv_heads, int head_dim,
+                                            int max_seq) {
+    return one_pass_ipk(n_heads, n_kv_heads, head_dim, max_seq) > 0;
+}
+
+bool attention_one_pass_launch(bf16 *out, const bf16 *q, const bf16 *k, const bf16 *v,
+                               const bf16 *q_norm_w, const bf16 *k_norm_w, bf16 *key_cache,
+                               bf16 *value_cache, void *ws, int *err, const int *d_pos,
+                               int n_heads, int n_kv_heads, int head_dim, float eps, float theta,
+                               int max_seq, float scale, hipStream_t stream) {
+    const int ipk = one_pass_ipk(n_heads, n_kv_heads, head_dim, max_seq);
+    if (ipk <= 0)
+        return llm_fail("attention_one_pass: no one-pass attention for %d/%d heads of %d over %d "
+                        "positions on this device", n_heads, n_kv_heads, head_dim, max_seq);
+    const void *ptrs[] = {out, q, k, v, q_norm_w, k_norm_w, key_cache, value_cache, ws, err,
+                          d_pos};
+    for (const void *p : ptrs)
+        if (!p) return llm_fail("attention_one_pass: null pointer argument");
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(q_norm_w) ||
+        !aligned16(k_norm_w) || !aligned16(key_cache) || !aligned16(value_cache) ||
+        ((uintptr_t)ws & 255))
+        return llm_fail("attention_one_pass: q, k, v, the norm weights and the caches must be "
+                        "16-byte aligned and the workspace 256-byte aligned");
+    OnePassArgs o;
+    memset(&o, 0, sizeof o);
+    AttnArgs &a = o.r.at;
+    a.out = out;
+    a.q = q;
+    a.kc = key_cache;
+    a.vc = value_cache;
+    a.d_pos = d_pos;
+    a.n_heads = n_heads;
+    a.n_kv_heads = n_kv_heads;
+    a.max_seq = max_seq;
+    a.max_blocks = (int)ceil_div((size_t)max_seq, ATT_B);
+    a.scale = scale;
+    o.r.k = k;
+    o.r.v = v;
+    o.r.qn = q_norm_w;
+    o.r.kn = k_norm_w;
+    o.r.kc_w = key_cache;
+    o.r.vc_w = value_cache;
+    o.r.eps = eps;
+    rope_inv_freq_table(theta, head_dim, o.r.inv_freq);
+    o.launches = (unsigned long long *)ws;
+    o.tstats = (unsigned long long *)((char *)ws + OP_HEADER);
+    o.tpart = o.tstats + (size_t)n_heads * a.max_blocks * 2;
+    o.err = err;
+    o.ipk = ipk;
+    const int rep = n_heads / n_kv_heads;
+    o.cpi = (rep * head_dim + ipk - 1) / ipk;
+    const int grid = n_kv_heads * ipk;
+    switch (rep) {
+    case 1: attn_one_pass_kernel<1><<<grid, OP_THREADS, 0, stream>>>(o); break;
+    case 2: attn_one_pass_kernel<2><<<grid, OP_THREADS, 0, stream>>>(o); break;
+    case 4: attn_one_pass_kernel<4><<<grid, OP_THREADS, 0, stream>>>(o); break;
+    default: attn_one_pass_kernel<8><<<grid, OP_THREADS, 0, stream>>>(o); break;
+    }
+    return LAUNCH_OK();
+}
+
+extern "C" void qk_norm_rope_attention_one_pass(bf16 *out, const bf16 *q, const bf16 *k,
+                                                const bf16 *v, const bf16 *q_norm_w,
+                                                const bf16 *k_norm_w, bf16 *key_cache,
+                                                bf16 *value_cache, void *ws, int *err,
+                                                const int *d_pos, int n_heads, int n_kv_heads,
+                                                int head_dim, float eps, float theta,
+                                                int max_seq, float scale, hipStream_t stream) {
+    attention_one_pass_launch(out, q, k, v, q_norm_w, k_norm_w, key_cache, value_cache, ws, err,
+                              d_pos, n_heads, n_kv_heads, head_dim, eps, theta, max_seq, scale,
+                              stream);
 }
 
 template <int D, int REP>

@@ -52,11 +52,11 @@ class RunState(ctypes.Structure):
                 ("pos_base", _vp), ("error_flag", _vp), ("loop_graph", _vp), ("step_mode", _i),
                 ("persistent", _i), ("step_ws", _vp), ("layers_dev", _vp), ("step_grid", _i),
                 ("next_token_valid", _i), ("step_trace", ctypes.POINTER(ctypes.c_longlong)),
-                ("attn_mode", _i)]
+                ("attn_mode", _i), ("attn_one_pass_ws", _vp)]
 
 
 STEP_MODES = {"auto": 0, "graph": 1, "persistent": 2}
-ATTN_MODES = {"auto": 0, "separate": 1, "in_scores": 2}
+ATTN_MODES = {"auto": 0, "separate": 1, "in_scores": 2, "one_pass": 3}
 
 
 _PC, _PW, _PS = ctypes.POINTER(Config), ctypes.POINTER(Weights), ctypes.POINTER(RunState)

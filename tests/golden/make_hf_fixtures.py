@@ -11,6 +11,7 @@ tests/golden/hf_small_qwen3_dumps.npz, the small model's activation dumps (the r
 tests/golden/hf_qwen3_06b_greedy.npz, the Qwen3-0.6B shapes (QWEN3_06B, qwen3_np_weights(., 0)),
 the bench's 5 seeded prompt ids:
   greedy, greedy_gap  [256]; top_values, top_indices [256, 8]: the 8 largest logits per step
+  full_steps [9]; full_logits [9, vocab] bf16 bits: every logit at steps 0, 32, ..., 224, 255
 
 These pin what no closed form does: the HF fp32/bf16 CPU arithmetic end to end (the e2e logits
 within 2e-2 and the greedy sequence up to near ties). The fixtures are data; this script is the
@@ -34,6 +35,7 @@ GREEDY_STEPS = 40
 # tokens; per step the top-2 gap and the 8 largest logits (values, indices).
 GREEDY_06B_STEPS = 256
 TOPK = 8
+FULL_06B_STEPS = list(range(0, GREEDY_06B_STEPS, 32)) + [GREEDY_06B_STEPS - 1]
 
 
 def hf_model(c, w, max_pos=64):
@@ -186,13 +188,23 @@ def qwen06b_fixture():
         gaps.append(float(top.values[0] - top.values[1]))
         top_v.append(top.values.numpy())
         top_i.append(top.indices.numpy().astype(np.int32))
+    # HF's logits are the bf16 lm_head output (generate hands them out widened to fp32, which is
+    # exact): kept as their bf16 bits, all 151936 of them
+    full = []
+    for i in FULL_06B_STEPS:
+        row = out.logits[i][0]
+        b = row.to(torch.bfloat16)
+        assert torch.equal(b.float(), row.float()), "logits are not bf16 values"
+        full.append(b.contiguous().view(torch.int16).numpy().view(np.uint16))
+    full = np.stack(full)
     meta = {"transformers": transformers.__version__, "torch": torch.__version__,
             "dtype": "bfloat16", "attn_implementation": "eager", "device": "cpu",
             "model": dict(c), "weights": "tests/conftest.py qwen3_np_weights(QWEN3_06B, 0)",
             "prompt": prompt}
     np.savez_compressed(os.path.join(HERE, "hf_qwen3_06b_greedy.npz"), greedy=greedy,
                         greedy_gap=np.array(gaps, np.float32), top_values=np.array(top_v),
-                        top_indices=np.array(top_i), meta=np.array(json.dumps(meta)))
+                        top_indices=np.array(top_i), full_steps=np.array(FULL_06B_STEPS, np.int32),
+                        full_logits=full, meta=np.array(json.dumps(meta)))
     print("wrote hf_qwen3_06b_greedy.npz:", greedy[:8], "min gap", min(gaps))
 
 

@@ -403,6 +403,74 @@ def test_qk_norm_rope_attention_fused(gpu, oracle, hq, hkv, D, pos, max_seq):
         kc, vc = ekc, evc
 
 
+ONE_PASS_CASES = [(16, 8, 128, 0, 4096), (16, 8, 128, 63, 4096), (16, 8, 128, 64, 4096),
+                  (16, 8, 128, 260, 4096), (16, 8, 128, 4095, 4096), (32, 8, 128, 8192, 8448),
+                  (32, 8, 128, 8447, 8448), (32, 8, 128, 30001, 32768), (8, 8, 128, 100, 512),
+                  (8, 1, 128, 130, 512), (8, 1, 128, 9000, 9100), (2, 2, 128, 301, 512),
+                  (16, 2, 128, 2000, 2048), (3, 3, 128, 4100, 4200)]
+
+
+@pytest.mark.parametrize("hq,hkv,D,pos,max_seq", ONE_PASS_CASES)
+def test_qk_norm_rope_attention_one_pass(gpu, oracle, hq, hkv, D, pos, max_seq):
+    """qk_norm_rope_attention_one_pass (QK-norm + RoPE + attention in one launch, the
+    workgroups of a kv head handing block statistics and partial outputs to each other): the
+    output is bit-identical to the oracle's GPU order of the two steps, the caches equal the
+    oracle's (row pos written, every other row unchanged), q and k are not rewritten and the
+    error flag stays 0. Five calls on one workspace (its launch counter tags the handoffs): the
+    case, an earlier position, the case again, the first position and the case once more, each
+    with new inputs, so a stale word of an earlier call would be read as current."""
+    import torch
+    if not gpu.attention_one_pass_supported(hq, hkv, D, max_seq):
+        pytest.skip("no one-pass attention for this shape on this device")
+    ident(f"one-pass attention {hq}/{hkv} D{D} pos{pos} max_seq{max_seq}")
+    rng = np.random.default_rng(hq * 7919 + hkv * 31 + D + pos + 17)
+    kc = rand_bf16(rng, (max_seq, hkv * D))
+    vc = rand_bf16(rng, (max_seq, hkv * D))
+    kcd, vcd = dev(kc), dev(vc)
+    ws = torch.zeros(gpu.attention_one_pass_bytes(hq, D, max_seq), dtype=torch.uint8,
+                     device="cuda")
+    err = dev_i32([0])
+    scale = float(np.float32(1.0 / np.sqrt(D)))
+    qn = rand_bf16(rng, D, 0.1, 1.0)
+    kn = rand_bf16(rng, D, 0.1, 1.0)
+    for p in [pos, pos // 2, pos, 0, pos]:
+        q = rand_bf16(rng, hq * D)
+        k = rand_bf16(rng, hkv * D)
+        v = rand_bf16(rng, hkv * D)
+        qd, kd = dev(q), dev(k)
+        out = dev(np.zeros(hq * D, np.uint16))
+        gpu.qk_norm_rope_attention_one_pass(out, qd, kd, dev(v), dev(qn), dev(kn), kcd, vcd, ws,
+                                            err, dev_i32([p]), hq, hkv, D, 1e-6, 1e6, max_seq,
+                                            scale)
+        eq, ek, ekc, evc = oracle.qk_norm_rope_rows(q[None], k[None], v[None], qn, kn, kc, vc, [p],
+                                                    hq, hkv, D, 1e-6, 1e6, oracle.GPU_ORDER)
+        want = oracle.attention(eq.reshape(-1), ekc, evc, hq, hkv, D, p, scale, oracle.GPU_ORDER)
+        got = host(out)
+        assert int(err.cpu()[0]) == 0, p
+        assert np.array_equal(got, want), p
+        assert np.array_equal(host(kcd).reshape(kc.shape), ekc), p
+        assert np.array_equal(host(vcd).reshape(vc.shape), evc), p
+        assert np.array_equal(host(qd), q) and np.array_equal(host(kd), k)
+        kc, vc = ekc, evc
+
+
+def test_qk_norm_rope_attention_one_pass_rejects(gpu):
+    """Shapes the one-pass attention is not built for are refused with a message, and report
+    themselves as unsupported."""
+    import torch
+    ws = torch.zeros(1 << 20, dtype=torch.uint8, device="cuda")
+    x = dev(np.zeros(4096, np.uint16))
+    err = dev_i32([0])
+    for hq, hkv, D, max_seq in [(4, 2, 64, 16), (6, 2, 128, 16), (16, 8, 128, 40000)]:
+        assert not gpu.attention_one_pass_supported(hq, hkv, D, max_seq)
+        with pytest.raises(gpu.LlmError):
+            gpu.qk_norm_rope_attention_one_pass(x, x, x, x, x, x, x, x, ws, err, dev_i32([0]), hq,
+                                                hkv, D, 1e-6, 1e6, max_seq, 0.1)
+    with pytest.raises(gpu.LlmError):  # no norm weights
+        gpu.qk_norm_rope_attention_one_pass(x, x, x, x, None, None, x, x, ws, err, dev_i32([0]),
+                                            4, 2, 128, 1e-6, 1e6, 16, 0.1)
+
+
 def test_qk_norm_rope_attention_fused_rejects(gpu):
     """Shapes the kernels are not built for are refused with a message."""
     import torch
