@@ -126,13 +126,17 @@ typedef struct {
                                (qk_norm_rope_attention_one_pass) */
     void *attn_one_pass_ws; /* the one-pass attention's workspace (zeroed at allocation; NULL
                                where the shapes have no one-pass attention) */
+    float *rope_table;      /* [head_dim] cos then sin of the RoPE rotation at *pos, computed
+                               once per step for the in-scores attention of every layer */
 } RunState;
 
 /* RunState::attn_mode. ATTN_AUTO takes ATTN_IN_SCORES when the longest history (max_seq) has at
- * most 256 (64-position block, kv head) items: every item then recomputes the query heads'
- * QK-norm + RoPE cheaply (Qwen3-0.6B graph step, 269 positions: +3% tokens/s), else
- * ATTN_SEPARATE (Qwen3-4B at 8448 positions: 418 tokens/s against 407 for ATTN_IN_SCORES and
- * 412 for ATTN_ONE_PASS). ATTN_ONE_PASS is taken only when asked for. */
+ * most 256 (64-position block, kv head) items, or when head_dim <= 128 and at most 4 query heads
+ * share a kv head: every item then applies the query heads' QK-norm + RoPE with the step's RoPE
+ * table (RunState::rope_table, one launch per step) and the scores kernel keeps five workgroups
+ * per CU (Qwen3-0.6B graph step, 269 positions: +3% tokens/s; Qwen3-4B at 8448 positions: 420.6
+ * tokens/s against 416.1 for ATTN_SEPARATE and 412.2 for ATTN_ONE_PASS). Otherwise
+ * ATTN_SEPARATE. ATTN_ONE_PASS is taken only when asked for. */
 enum { ATTN_AUTO = 0, ATTN_SEPARATE = 1, ATTN_IN_SCORES = 2, ATTN_ONE_PASS = 3 };
 
 /* How capture_graph prepares the step. STEP_AUTO: the persistent step kernel (one cooperative

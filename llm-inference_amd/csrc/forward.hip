@@ -48,7 +48,8 @@ extern "C" void alloc_run_state_seq(RunState *s, const Config *cfg, int max_seq)
               dmalloc((void **)&s->next_token, 4) && dmalloc((void **)&s->pos, 4) &&
               dmalloc(&s->argmax_partials, (size_t)argmax_partial_count() * 8) &&
               dmalloc((void **)&s->pos_base, 4) && dmalloc((void **)&s->error_flag, 4) &&
-              dmalloc(&s->step_ws, step_workspace_bytes(cfg));
+              dmalloc(&s->step_ws, step_workspace_bytes(cfg)) &&
+              dmalloc((void **)&s->rope_table, (size_t)cfg->head_dim * 4);
     if (ok && attention_one_pass_supported(cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, max_seq))
         ok = dmalloc(&s->attn_one_pass_ws,
                      attention_one_pass_bytes(cfg->n_heads, cfg->head_dim, max_seq));
@@ -65,7 +66,7 @@ extern "C" void free_run_state(RunState *s) {
                     s->att, s->key_cache, s->value_cache, s->hb, s->tap1, s->tap2,
                     s->logits, s->next_token, s->pos, s->argmax_partials, s->token_out,
                     s->pos_base, s->error_flag, s->step_ws, s->layers_dev,
-                    s->attn_one_pass_ws};
+                    s->attn_one_pass_ws, s->rope_table};
     for (void *b : bufs)
         if (b) HIP_OK(hipFree(b));
     if (s->graph) HIP_OK(hipGraphExecDestroy(s->graph));
@@ -120,12 +121,17 @@ static bool forward_kernels(const Config *cfg, const Weights *w, RunState *s) {
     const bool one_pass = !dumping && s->attn_mode == ATTN_ONE_PASS;
     if (one_pass && !s->attn_one_pass_ws)
         return llm_fail("forward: no one-pass attention for these shapes");
-    const bool fuse_attn = !dumping && !one_pass &&
-                           (s->attn_mode == ATTN_IN_SCORES ||
-                            (s->attn_mode == ATTN_AUTO && attn_items <= 256));
+    const int rep = cfg->n_heads / cfg->n_kv_heads;
+    const bool fuse_attn =
+        !dumping && !one_pass &&
+        (s->attn_mode == ATTN_IN_SCORES ||
+         (s->attn_mode == ATTN_AUTO && (attn_items <= 256 || (D <= 128 && rep <= 4))));
     bf16 *tap1 = dumping ? s->tap1 : nullptr, *tap2 = dumping ? s->tap2 : nullptr;
     embedding_checked(s->x, w->embed, s->next_token, H, cfg->vocab_size, s->error_flag, st);
     dump_bf16("embed", s->x, H);
+    // The in-scores attention of every layer reads the RoPE table of this position from one
+    // launch instead of recomputing it in each of its items.
+    if (fuse_attn && !rope_table_launch(s->rope_table, s->pos, D, cfg->rope_theta, st)) return false;
     for (int l = 0; l < cfg->n_layers && !llm_has_error(); l++) {
         const LayerWeights *L = &w->layers[l];
         bf16 *kc = s->key_cache + (size_t)l * s->max_seq * kv_dim;
@@ -152,7 +158,7 @@ static bool forward_kernels(const Config *cfg, const Weights *w, RunState *s) {
             qk_norm_rope_attention_launch(s->attn_out, s->q, s->k, s->v, L->q_norm, L->k_norm, kc,
                                           vc, s->att, s->pos, cfg->n_heads, cfg->n_kv_heads, D,
                                           cfg->rms_norm_eps, cfg->rope_theta, s->max_seq, scale,
-                                          st);
+                                          st, s->rope_table);
         } else {
             qk_norm_rope_forward(s->q, s->k, s->v, L->q_norm, L->k_norm, kc, vc, s->pos,
                                  cfg->n_heads, cfg->n_kv_heads, D, cfg->rms_norm_eps,

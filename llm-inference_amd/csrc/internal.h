@@ -15,7 +15,6 @@ int argmax_partial_count();
 // inv_freq_j = 1 / fp32(pow(theta, fp32(2j / D))) for j < D/2 (D <= 256), cached per (theta, D).
 void rope_inv_freq_table(float theta, int D, float *out);
 
-// qk_norm_rope_attention_forward, reporting whether it launched.
 // qk_norm_rope_attention_one_pass, reporting whether it launched.
 bool attention_one_pass_launch(bf16 *out, const bf16 *q, const bf16 *k, const bf16 *v,
                                const bf16 *q_norm_w, const bf16 *k_norm_w, bf16 *key_cache,
@@ -23,8 +22,16 @@ bool attention_one_pass_launch(bf16 *out, const bf16 *q, const bf16 *k, const bf
                                int n_heads, int n_kv_heads, int head_dim, float eps, float theta,
                                int max_seq, float scale, hipStream_t stream);
 
+// qk_norm_rope_attention_forward, reporting whether it launched; with rope_table (the
+// rope_table_launch output at *d_pos), the kernel reads the RoPE table instead of computing it.
 bool qk_norm_rope_attention_launch(bf16 *out, const bf16 *q, const bf16 *k, const bf16 *v,
                                    const bf16 *q_norm_w, const bf16 *k_norm_w, bf16 *key_cache,
                                    bf16 *value_cache, float *att, const int *d_pos, int n_heads,
                                    int n_kv_heads, int head_dim, float eps, float theta,
-                                   int max_seq, float scale, hipStream_t stream);
+                                   int max_seq, float scale, hipStream_t stream,
+                                   const float *rope_table = nullptr);
+
+// The RoPE table at *d_pos into table[0, head_dim): cos then sin of the head_dim / 2 rotation
+// pairs, the values rope_table computes in the kernels (one launch serves every layer).
+bool rope_table_launch(float *table, const int *d_pos, int head_dim, float theta,
+                       hipStream_t stream);

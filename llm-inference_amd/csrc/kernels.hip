@@ -992,9 +992,38 @@ struct AttnRopeArgs {
     AttnArgs at;
     const bf16 *k, *v, *qn, *kn;  // at.q is the query before QK-norm + RoPE
     bf16 *kc_w, *vc_w;            // the caches, writable (row pos)
+    const float *table;           // the RoPE table at *d_pos (rope_table_kernel), or NULL
     float eps;
     float inv_freq[128];
 };
+
+// The RoPE table at *d_pos, once for every layer of a step: table[j] = cos and table[D/2 + j] =
+// sin of fp32(pos * inv_freq_j) as rope_table computes them (double sincos, rounded to fp32 and
+// then to bf16), j < D/2.
+struct RopeFreqArgs {
+    float inv_freq[128];
+};
+__global__ __launch_bounds__(128) void rope_table_kernel(float *table, const int *d_pos,
+                                                         RopeFreqArgs f, int half) {
+    const int j = threadIdx.x;
+    if (j < half) {
+        const float angle = (float)*d_pos * f.inv_freq[j];
+        double sn, cs;
+        sincos_d((double)angle, &sn, &cs);
+        table[j] = round_bf((float)cs);
+        table[half + j] = round_bf((float)sn);
+    }
+}
+
+bool rope_table_launch(float *table, const int *d_pos, int head_dim, float theta,
+                       hipStream_t stream) {
+    if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+        return llm_fail("rope_table: head_dim %d is not 64, 128 or 256", head_dim);
+    RopeFreqArgs f;
+    rope_inv_freq_table(theta, head_dim, f.inv_freq);
+    rope_table_kernel<<<1, 128, 0, stream>>>(table, d_pos, f, head_dim / 2);
+    return LAUNCH_OK();
+}
 
 // The rope inputs of one wave (the raw head rows and norm weights), requested before the key
 // rows so that they are not behind them (loads complete in order), and the RoPE table.
@@ -1087,8 +1116,14 @@ __device__ __forceinline__ void rope_finish(const AttnRopeArgs &r, int g, int po
     }
 }
 
-template <int D, int REP>
-__global__ __launch_bounds__(256) void attn_rope_scores_kernel(AttnRopeArgs r) {
+// TABLE: the RoPE table comes from r.table (a small load issued with the rope inputs) instead of
+// being computed in double precision by every item. The kernel then fits 96 registers without
+// spills for D <= 128 and REP <= 4 (five workgroups per CU instead of four: Qwen3-4B's 1056 items
+// at 8448 positions are resident in one wave of 1280 slots) and its items' rope chain is shorter.
+template <int D, int REP, bool TABLE>
+__global__ __launch_bounds__(256)
+__attribute__((amdgpu_waves_per_eu(TABLE && D <= 128 && REP <= 4 ? 5 : 1)))
+void attn_rope_scores_kernel(AttnRopeArgs r) {
     constexpr int LP = D / 8, PPW = 64 / LP, PER_WAVE = ATT_B / 4, ITERS = PER_WAVE / PPW;
     const AttnArgs &a = r.at;
     __shared__ float sc[REP][ATT_B];
@@ -1104,7 +1139,23 @@ __global__ __launch_bounds__(256) void attn_rope_scores_kernel(AttnRopeArgs r) {
         const bool last = b == nb - 1;
         RopeIn<D> in;
         const bool roper = rope_request<D, REP>(r, g, pos, last, in);
-        const LaneFreq<D> freq = lane_freq<D>(r.inv_freq);
+        LaneFreq<D> freq{};
+        if constexpr (TABLE) {
+            constexpr int HALF = D / 2;
+            const __amdgpu_buffer_rsrc_t tr = __builtin_amdgcn_make_buffer_rsrc(
+                (void *)r.table, (short)0, 2 * HALF * 4, BUFFER_FLAGS);
+#pragma unroll
+            for (int m = 0; m < RopeShape<D>::NJ; m++) {
+                const int j = lane + 64 * m;  // entries past HALF read as zeros
+                in.cs[m] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                    tr, 4 * (j < HALF ? j : 2 * HALF), 0, 0));
+                in.sn[m] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                    tr, 4 * (j < HALF ? HALF + j : 2 * HALF), 0, 0));
+            }
+            __builtin_amdgcn_sched_barrier(0);  // ahead of the key rows
+        } else {
+            freq = lane_freq<D>(r.inv_freq);
+        }
         u32x4 kv[ITERS];
 #pragma unroll
         for (int it = 0; it < ITERS; it++) {
@@ -1112,7 +1163,7 @@ __global__ __launch_bounds__(256) void attn_rope_scores_kernel(AttnRopeArgs r) {
             kv[it] = t < pos ? ld16_nt(a.kc + (size_t)t * kv_dim + g * D + 8 * L) : u32x4{0, 0, 0, 0};
         }
         // the table while the rows stream (arithmetic only)
-        if (roper) rope_table<D>(pos, freq, in.cs, in.sn);
+        if (!TABLE && roper) rope_table<D>(pos, freq, in.cs, in.sn);
         __syncthreads();  // qk_s of the previous item has been read
         if (roper) rope_finish<D, REP>(r, g, pos, in, qk_s, qk_s + REP * (D / 8));
         __syncthreads();
@@ -1902,8 +1953,10 @@ extern "C" void qk_norm_rope_attention_one_pass(bf16 *out, const bf16 *q, const 
 template <int D, int REP>
 static void launch_attention_t(const AttnArgs &a, int grid, hipStream_t stream,
                                const AttnRopeArgs *rope = nullptr) {
-    if (rope)
-        attn_rope_scores_kernel<D, REP><<<grid, 256, 0, stream>>>(*rope);
+    if (rope && rope->table)
+        attn_rope_scores_kernel<D, REP, true><<<grid, 256, 0, stream>>>(*rope);
+    else if (rope)
+        attn_rope_scores_kernel<D, REP, false><<<grid, 256, 0, stream>>>(*rope);
     else
         attn_scores_kernel<D, REP><<<grid, 256, 0, stream>>>(a);
     if (!LAUNCH_OK()) return;
@@ -1911,6 +1964,26 @@ static void launch_attention_t(const AttnArgs &a, int grid, hipStream_t stream,
     if (!LAUNCH_OK()) return;
     attn_combine_kernel<D><<<a.n_heads * (D / COMBINE_COLS), 256, 0, stream>>>(a);
     LAUNCH_OK();
+}
+
+// The caller's `att` must hold attention_workspace_floats() floats, more than the reference's
+// [n_heads, max_seq] scores: a caller that sized it the reference's way gets an error, not an
+// overrun, wherever the runtime knows the allocation holding `att` (a buffer carved out of a
+// larger allocation passes if that allocation is large enough).
+static bool check_att_size(const float *att, int n_heads, int head_dim, int max_seq) {
+    hipDeviceptr_t base = nullptr;
+    size_t bytes = 0;
+    if (hipMemGetAddressRange(&base, &bytes, (hipDeviceptr_t)att) != hipSuccess || !base) {
+        (void)hipGetLastError();  // not a runtime allocation: nothing to check against
+        return true;
+    }
+    const size_t need = attention_workspace_floats(n_heads, head_dim, max_seq) * sizeof(float);
+    const size_t avail = bytes - (size_t)((const char *)att - (const char *)base);
+    if (avail < need)
+        return llm_fail("attention: att has room for %zu bytes, the workspace needs %zu "
+                        "(attention_workspace_floats(%d, %d, %d) floats)",
+                        avail, need, n_heads, head_dim, max_seq);
+    return true;
 }
 
 static bool attention_args(AttnArgs &a, int &grid, bf16 *out, const bf16 *q,
@@ -1928,6 +2001,7 @@ static bool attention_args(AttnArgs &a, int &grid, bf16 *out, const bf16 *q,
     if (max_seq <= 0) return llm_fail("attention: max_seq %d must be positive", max_seq);
     if (!aligned16(q) || !aligned16(key_cache) || !aligned16(value_cache) || !aligned16(att))
         return llm_fail("attention: q, the caches and att must be 16-byte aligned");
+    if (att && !check_att_size(att, n_heads, head_dim, max_seq)) return false;
     a.out = out;
     a.q = q;
     a.kc = key_cache;
@@ -2002,7 +2076,8 @@ bool qk_norm_rope_attention_launch(bf16 *out, const bf16 *q, const bf16 *k, cons
                                    const bf16 *q_norm_w, const bf16 *k_norm_w, bf16 *key_cache,
                                    bf16 *value_cache, float *att, const int *d_pos, int n_heads,
                                    int n_kv_heads, int head_dim, float eps, float theta,
-                                   int max_seq, float scale, hipStream_t stream) {
+                                   int max_seq, float scale, hipStream_t stream,
+                                   const float *rope_table) {
     AttnRopeArgs r;
     memset(&r, 0, sizeof r);
     int grid = 0;
@@ -2020,6 +2095,7 @@ bool qk_norm_rope_attention_launch(bf16 *out, const bf16 *q, const bf16 *k, cons
     r.kn = k_norm_w;
     r.kc_w = key_cache;
     r.vc_w = value_cache;
+    r.table = rope_table;
     r.eps = eps;
     rope_inv_freq_table(theta, head_dim, r.inv_freq);
     const int rep = n_heads / n_kv_heads;

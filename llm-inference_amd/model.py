@@ -52,7 +52,8 @@ class RunState(ctypes.Structure):
                 ("pos_base", _vp), ("error_flag", _vp), ("loop_graph", _vp), ("step_mode", _i),
                 ("persistent", _i), ("step_ws", _vp), ("layers_dev", _vp), ("step_grid", _i),
                 ("next_token_valid", _i), ("step_trace", ctypes.POINTER(ctypes.c_longlong)),
-                ("attn_mode", _i), ("attn_one_pass_ws", _vp)]
+                ("attn_mode", _i), ("attn_one_pass_ws", _vp),
+                ("rope_table", ctypes.POINTER(ctypes.c_float))]
 
 
 STEP_MODES = {"auto": 0, "graph": 1, "persistent": 2}

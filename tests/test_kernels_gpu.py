@@ -471,6 +471,29 @@ def test_qk_norm_rope_attention_one_pass_rejects(gpu):
                                             4, 2, 128, 1e-6, 1e6, 16, 0.1)
 
 
+def test_attention_rejects_a_workspace_too_small(gpu):
+    """The C-ABI guard on `att`: a workspace sized for fewer positions than max_seq (here a
+    RunState's own att, allocated for 64 positions, passed with max_seq 4096, as a caller sizing
+    it [n_heads, max_seq] the reference's way would under-size it) is an error, not an overrun;
+    the same buffer at its own size runs."""
+    from llm_inference_amd import model
+    cfg = model.make_config(hidden_size=512, intermediate_size=1024, n_layers=1, n_heads=8,
+                            n_kv_heads=4, vocab_size=256, max_seq_len=64)
+    dec = model.Decoder(cfg, ("synth", 1, 0.02, 0.1))
+    try:
+        D, hq, hkv = 128, 8, 4
+        q = dev(np.zeros(hq * D, np.uint16))
+        kc = dev(np.zeros((4096, hkv * D), np.uint16))
+        out = dev(np.zeros(hq * D, np.uint16))
+        att = int(dec.s.att)
+        with pytest.raises(gpu.LlmError, match="att has room"):
+            gpu.attention_forward(out, q, kc, kc, att, hq, hkv, D, dev_i32([10]), 4096, 0.1)
+        gpu.attention_forward(out, q, kc, kc, att, hq, hkv, D, dev_i32([10]), 64, 0.1)
+        host(out)
+    finally:
+        dec.close()
+
+
 def test_qk_norm_rope_attention_fused_rejects(gpu):
     """Shapes the kernels are not built for are refused with a message."""
     import torch
