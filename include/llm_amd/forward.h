@@ -128,6 +128,8 @@ typedef struct {
                                where the shapes have no one-pass attention) */
     float *rope_table;      /* [head_dim] cos then sin of the RoPE rotation at *pos, computed
                                once per step for the in-scores attention of every layer */
+    int step_switch_pos;    /* with the persistent kernel prepared: positions below this run it,
+                               positions from it on the hipGraph step (set by capture_graph) */
 } RunState;
 
 /* RunState::attn_mode. ATTN_AUTO takes ATTN_IN_SCORES when the longest history (max_seq) has at
@@ -139,11 +141,15 @@ typedef struct {
  * ATTN_SEPARATE. ATTN_ONE_PASS is taken only when asked for. */
 enum { ATTN_AUTO = 0, ATTN_SEPARATE = 1, ATTN_IN_SCORES = 2, ATTN_ONE_PASS = 3 };
 
-/* How capture_graph prepares the step. STEP_AUTO: the persistent step kernel (one cooperative
- * launch per forward; generate_greedy runs all its tokens in one launch) when the shapes have a
- * specialisation and the hidden size is at most 2048 (Qwen3-0.6B and 1.7B, where it is the
- * faster step), else a hipGraph of the per-layer kernels. STEP_GRAPH: always the hipGraph.
- * STEP_PERSISTENT: the persistent kernel (also at 4B) or an error. */
+/* How capture_graph prepares the step. STEP_AUTO: where the shapes have a specialisation
+ * (Qwen3-0.6B, 1.7B, 4B), the persistent step kernel (one cooperative launch per forward;
+ * generate_greedy runs its tokens in one launch) for the positions below
+ * RunState::step_switch_pos, and a hipGraph of the per-layer kernels from there on: the kernel's
+ * attention runs one workgroup per query head, so its cost grows with the history faster than
+ * the graph's (crossover 736 / 480 / 448 positions at 0.6B / 1.7B / 4B; 5-token prompt: 2356 /
+ * 1121 / 578 tokens/s against 1278 / 893 / 492). Other shapes: the hipGraph. STEP_GRAPH:
+ * always the hipGraph. STEP_PERSISTENT: the persistent kernel at every position (max_seq at
+ * most 8192) or an error. */
 enum { STEP_AUTO = 0, STEP_GRAPH = 1, STEP_PERSISTENT = 2 };
 
 /* src/loader.cu:105-139 (config.json, generation_config.json) */

@@ -353,20 +353,32 @@ extern "C" void capture_graph(const Config *cfg, const Weights *w, RunState *s) 
         s->loop_graph = nullptr;
     }
     s->persistent = 0;
+    s->step_switch_pos = 0;
     // while dumping, the step runs eagerly (the reference captures only without --dump,
     // src/main.cu:253): nothing is captured, and forward() dumps as it goes
     if (dump_enabled()) return;
-    const bool want = s->step_mode == STEP_PERSISTENT ||
-                      (s->step_mode == STEP_AUTO && step_kernel_preferred(cfg));
-    if (want && step_kernel_supported(cfg, s->max_seq)) {
-        prepare_persistent(cfg, w, s);
+    if (s->step_mode == STEP_PERSISTENT) {
+        if (!step_kernel_supported(cfg, s->max_seq)) {
+            llm_fail("capture_graph: no persistent step kernel for these shapes");
+            return;
+        }
+        if (prepare_persistent(cfg, w, s)) s->step_switch_pos = s->max_seq;
         return;
     }
-    if (s->step_mode == STEP_PERSISTENT) {
-        llm_fail("capture_graph: no persistent step kernel for these shapes");
-        return;
+    // STEP_AUTO: the step kernel for the positions below its switch position, the hipGraph
+    // from there on (captured only when the cache reaches that far)
+    if (s->step_mode == STEP_AUTO && step_kernel_available(cfg)) {
+        if (!prepare_persistent(cfg, w, s)) return;
+        const int sw = step_kernel_switch_pos(cfg);
+        s->step_switch_pos = sw < s->max_seq ? sw : s->max_seq;
+        if (s->step_switch_pos >= s->max_seq) return;
     }
     capture(s->stream, &s->graph, step_body, &c);
+}
+
+// Whether the step at `pos` runs the persistent kernel (else the hipGraph or the eager step).
+static bool persistent_at(const RunState *s, int pos) {
+    return s->persistent && pos < s->step_switch_pos;
 }
 
 static bool check_token_pos(const Config *cfg, const RunState *s, int token, int pos) {
@@ -385,7 +397,7 @@ extern "C" void forward(const Config *cfg, const Weights *w, RunState *s, int to
     s->next_token_valid = 0;
     if (dump_enabled()) {
         forward_kernels(cfg, w, s);  // the dumps come from the eager step (src/main.cu:253)
-    } else if (s->persistent) {
+    } else if (persistent_at(s, pos)) {
         if (step_kernel_launch(cfg, step_args(cfg, w, s, 0), s->step_grid, s->stream))
             s->next_token_valid = 1;
     } else if (s->graph) {
@@ -478,30 +490,26 @@ extern "C" int generate_greedy(const Config *cfg, const Weights *w, RunState *s,
         s->next_token_valid = 1;
         return copy_tokens_out(cfg, s, n_steps, out_tokens);
     }
-    if (s->persistent) {
-        if (!ensure_token_capacity(s, n_steps)) return -1;
-        set_token_pos_kernel<<<1, 64, 0, s->stream>>>(s->next_token, s->pos, token, pos);
-        set_token_pos_kernel<<<1, 64, 0, s->stream>>>(s->error_flag, s->pos_base, 0, pos);
-        if (!LAUNCH_OK()) return -1;
-        StepArgs a = step_args(cfg, w, s, 1);
-        a.n_tokens = n_steps;  // one launch decodes every token
-        if (!step_kernel_launch(cfg, a, s->step_grid, s->stream)) return -1;
-        s->next_token_valid = 1;
-        if (!HIP_OK(hipMemcpyAsync(out_tokens, s->token_out, (size_t)n_steps * 4,
-                                   hipMemcpyDeviceToHost, s->stream)) ||
-            !HIP_OK(hipStreamSynchronize(s->stream)))
-            return -1;
-        return check_step_error(cfg, s) ? 0 : -1;
-    }
     if (!ensure_token_capacity(s, n_steps)) return -1;
-    if (!s->loop_graph) {
+    // the tokens at positions below the switch in one launch of the persistent kernel, the
+    // rest by the loop graph, which continues from the token and position that launch left
+    // on the device (both steps compute the same bits)
+    const int n_kernel = !persistent_at(s, pos) ? 0
+                         : pos + n_steps <= s->step_switch_pos ? n_steps
+                                                               : s->step_switch_pos - pos;
+    if (n_kernel < n_steps && !s->loop_graph) {
         StepCtx c{cfg, w, s};
         if (!capture(s->stream, &s->loop_graph, loop_body, &c)) return -1;
     }
     set_token_pos_kernel<<<1, 64, 0, s->stream>>>(s->next_token, s->pos, token, pos);
     set_token_pos_kernel<<<1, 64, 0, s->stream>>>(s->error_flag, s->pos_base, 0, pos);
     if (!LAUNCH_OK()) return -1;
-    for (int i = 0; i < n_steps; i++)
+    if (n_kernel > 0) {
+        StepArgs a = step_args(cfg, w, s, 1);
+        a.n_tokens = n_kernel;  // one launch decodes every token below the switch
+        if (!step_kernel_launch(cfg, a, s->step_grid, s->stream)) return -1;
+    }
+    for (int i = n_kernel; i < n_steps; i++)
         if (!HIP_OK(hipGraphLaunch(s->loop_graph, s->stream))) return -1;
     s->next_token_valid = 1;
     return copy_tokens_out(cfg, s, n_steps, out_tokens);

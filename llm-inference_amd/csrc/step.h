@@ -50,8 +50,12 @@ struct StepWorkspace {
 };
 
 size_t step_workspace_bytes(const Config *cfg);
+// STEP_PERSISTENT: the shapes have a specialisation and every position fits its attention.
 bool step_kernel_supported(const Config *cfg, int max_seq);
-// Whether STEP_AUTO takes the step kernel (where it is supported) over the hipGraph step.
-bool step_kernel_preferred(const Config *cfg);
+// The shapes have a specialisation (STEP_AUTO then runs it below step_kernel_switch_pos).
+bool step_kernel_available(const Config *cfg);
+// The first position at which STEP_AUTO runs the hipGraph step instead of the step kernel
+// (whose one workgroup per query head makes attention cost grow with the history faster).
+int step_kernel_switch_pos(const Config *cfg);
 int step_kernel_grid();
 bool step_kernel_launch(const Config *cfg, const StepArgs &args, int grid, hipStream_t stream);

@@ -276,20 +276,39 @@ struct Rows {
     }
 };
 
+// The staged input vector read from LDS chunk by chunk where a dot product uses it (lane l's
+// chunk k: 16 bytes at l + 64 k, as lds_chunks loads them), instead of NC registers held for
+// the whole phase: for long rows (the down rows' 6144 or 9728 columns) those registers would
+// otherwise spill.
+struct LdsX {
+    const u32x4 *v;
+    __device__ __forceinline__ u32x4 operator[](int k) const { return v[(tid_x() & 63) + 64 * k]; }
+};
+
 // The B row sums of a batch against xin (gemv_kernel arithmetic: per-lane fma over the chunks
 // in order, then the wave tree); lane l gets row scatter_row<B>(l) of the batch.
-template <int NC, int B>
-__device__ __forceinline__ float batch_sums(const Rows<NC, B> &b, const u32x4 (&xin)[NC]) {
+template <int NC, int B, class X>
+__device__ __forceinline__ float batch_sums(const Rows<NC, B> &b, const X &xin) {
     float part[B];
 #pragma unroll
-    for (int i = 0; i < B; i++) {
-        float acc = 0.0f;
+    for (int i = 0; i < B; i++) part[i] = 0.0f;
+    if constexpr (std::is_same_v<X, LdsX>) {
+        // each chunk read from LDS once for the batch's rows (same per-row order)
 #pragma unroll
-        for (int k = 0; k < NC; k++) acc = dot8(b.w[i][k], xin[k], acc);
-        part[i] = acc;
+        for (int k = 0; k < NC; k++) {
+            const u32x4 xk = xin[k];
+#pragma unroll
+            for (int i = 0; i < B; i++) part[i] = dot8(b.w[i][k], xk, part[i]);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < B; i++)
+#pragma unroll
+            for (int k = 0; k < NC; k++) part[i] = dot8(b.w[i][k], xin[k], part[i]);
     }
     return wave_sum_scatter<B>(part);
 }
+
 
 // Rows [r0, r1) against xin, B rows per batch, the first batch already in `cur` (requested a
 // phase ahead). With STREAM the next batch is requested before the current one is reduced
@@ -298,8 +317,8 @@ __device__ __forceinline__ float batch_sums(const Rows<NC, B> &b, const u32x4 (&
 // (lane j: row r0 + j, at most 64 rows): with KEEP it is replaced by epi's result for the row,
 // so a wave carries the residual rows it updates from one phase to the next. Lane
 // scatter_row<B>(k) computes batch row k, and scatter_row<B> is its own inverse.
-template <int NC, int B, bool STREAM, bool KEEP = false, class RowP, class Epi>
-__device__ __forceinline__ void wave_gemv(RowP rowp, int r0, int r1, const u32x4 (&xin)[NC],
+template <int NC, int B, bool STREAM, bool KEEP = false, class RowP, class X, class Epi>
+__device__ __forceinline__ void wave_gemv(RowP rowp, int r0, int r1, const X &xin,
                                           Rows<NC, B> &cur, Epi epi, uint32_t *own = nullptr) {
     const int lane = tid_x() & 63;
     auto finish = [&](float t, int r) {
@@ -807,8 +826,8 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
         pos = *gptr(a.pos);
         n_layers = a.n_layers;
         n_tokens = a.n_tokens;
-        if (pos < 0 || n_tokens < 1 || pos + n_tokens > a.max_seq || token < 0 ||
-            token >= a.vocab) {
+        if (pos < 0 || n_tokens < 1 || pos + n_tokens > a.max_seq || pos + n_tokens > S::NMAX ||
+            token < 0 || token >= a.vocab) {
             if (blockIdx.x == 0 && threadIdx.x == 0) *gptr(a.error_flag) = 1;
             return;  // every workgroup reads the same values and leaves at once
         }
@@ -1015,11 +1034,17 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
             stamp_wg(l, n_layers, 6, step);
             if (wg_o) {
                 if (o0 < o1) {
-                    u32x4 in[NCI];
-                    lds_chunks<NCI>(sm.vec, in);
-                    wave_gemv<NCI, S::B_DOWN, S::D_STREAM, true>(
-                        d_row(klayer(kargs(), l)), o0, o1, in, pf_d,
-                        residual(out_stage, wr0, tag_of(seq + 4)), &xown);
+                    if constexpr (S::X_LDS_DOWN) {
+                        wave_gemv<NCI, S::B_DOWN, S::D_STREAM, true>(
+                            d_row(klayer(kargs(), l)), o0, o1, LdsX{(const u32x4 *)sm.vec}, pf_d,
+                            residual(out_stage, wr0, tag_of(seq + 4)), &xown);
+                    } else {
+                        u32x4 in[NCI];
+                        lds_chunks<NCI>(sm.vec, in);
+                        wave_gemv<NCI, S::B_DOWN, S::D_STREAM, true>(
+                            d_row(klayer(kargs(), l)), o0, o1, in, pf_d,
+                            residual(out_stage, wr0, tag_of(seq + 4)), &xown);
+                    }
                 }
                 __syncthreads();
                 if ((tid_x() >> 6) == FW) publish_rows<H, S::REPLICAS>(kargs().tx, out_stage, wr0, wr1);
@@ -1168,6 +1193,11 @@ template <int H_, int I_, int HQ_, int HKV_>
 struct Shape {
     static constexpr int H = H_, I = I_, HQ = HQ_, HKV = HKV_;
     static constexpr int NMAX = 8192;  // positions a query head attends over (LDS scores)
+    // STEP_AUTO's switch to the hipGraph step: the crossover of the two steps' per-token time,
+    // measured on MI355X (64 greedy tokens after an N(0, 1) cache of 5..8100 positions): step
+    // kernel 424 + 0.53 us per position at 0.6B, 892 + 0.52 at 1.7B, 1730 + 0.72 at 4B; hipGraph
+    // 783 + 0.024, 1120 + 0.016, 2032 + 0.02 (us per token)
+    static constexpr int SWITCH_POS = H <= 1024 ? 736 : H <= 2048 ? 480 : 448;
     static constexpr int B_QKV = H <= 1024 ? 4 : 2;
     static constexpr int B_O = H <= 1024 ? 1 : (HQ * 128 <= 2048 ? 2 : 1);
     static constexpr int B_GU = H <= 1024 ? 2 : 1;
@@ -1187,6 +1217,10 @@ struct Shape {
     static constexpr bool POLLER = false;
     static constexpr bool O_STREAM = H > 1024;
     static constexpr bool D_STREAM = H > 1024;
+    // the down rows read the SwiGLU output from LDS (LdsX) instead of 19 chunk registers per
+    // lane, which spilled to scratch memory (95 VGPRs; the reloads queued behind the weight
+    // requests): 4B 363 -> 572 tokens/s. At 1.7B (12 chunks) the registers measure 4% faster.
+    static constexpr bool X_LDS_DOWN = H > 2048;
 };
 
 using Qwen3_06B = Shape<1024, 3072, 16, 8>;
@@ -1222,15 +1256,24 @@ size_t step_workspace_bytes(const Config *c) {
     return sizeof(StepWorkspace) + 4 * words;
 }
 
-bool step_kernel_supported(const Config *cfg, int max_seq) {
-    return step_kernel_for(cfg) != nullptr && max_seq <= 8192 && cfg->vocab_size > 0 &&
+bool step_kernel_available(const Config *cfg) {
+    return step_kernel_for(cfg) != nullptr && cfg->vocab_size > 0 &&
            step_grid_fits(cfg, step_kernel_grid());
 }
 
-// Measured on MI355X, 5-token prompt then 128 tokens: 0.6B 2330 tokens/s (step kernel) against
-// 1179 (hipGraph), 1.7B 1059 against 856, 4B 356 against 479: the 4B layers stream 202 MB
-// each, which the per-kernel GEMVs of the graph read faster than the step kernel's row batches.
-bool step_kernel_preferred(const Config *cfg) { return cfg->hidden_size <= 2048; }
+bool step_kernel_supported(const Config *cfg, int max_seq) {
+    return step_kernel_available(cfg) && max_seq <= 8192;
+}
+
+// Measured on MI355X, 5-token prompt then 128-256 tokens: 0.6B 2356 tokens/s (step kernel)
+// against 1278 (hipGraph), 1.7B 1121 against 893, 4B 578 against 492.
+int step_kernel_switch_pos(const Config *cfg) {
+#define SWITCH(S)                                                                           \
+    if (step_kernel_for(cfg) == (const void *)step_kernel<S>) return S::SWITCH_POS;
+    SWITCH(Qwen3_06B) SWITCH(Qwen3_17B) SWITCH(Qwen3_4B) SWITCH(SmallTest)
+#undef SWITCH
+    return 0;
+}
 
 int step_kernel_grid() {
     int dev = 0, cus = 0;

@@ -53,7 +53,7 @@ class RunState(ctypes.Structure):
                 ("persistent", _i), ("step_ws", _vp), ("layers_dev", _vp), ("step_grid", _i),
                 ("next_token_valid", _i), ("step_trace", ctypes.POINTER(ctypes.c_longlong)),
                 ("attn_mode", _i), ("attn_one_pass_ws", _vp),
-                ("rope_table", ctypes.POINTER(ctypes.c_float))]
+                ("rope_table", ctypes.POINTER(ctypes.c_float)), ("step_switch_pos", _i)]
 
 
 STEP_MODES = {"auto": 0, "graph": 1, "persistent": 2}
@@ -227,15 +227,32 @@ class Decoder:
         return self.s.stream
 
     def capture_graph(self, mode=None):
-        """Prepares the replayed step: the persistent step kernel ("auto" when the shapes have
-        a specialisation, or "persistent") or a hipGraph of the per-layer kernels ("graph")."""
+        """Prepares the replayed step: "auto" (the persistent step kernel below its switch
+        position where the shapes have a specialisation, the hipGraph of the per-layer kernels
+        from there on), "persistent" (the kernel at every position) or "graph"."""
         self.s.step_mode = STEP_MODES[mode or self.mode]
         lib().capture_graph(ctypes.byref(self.cfg), ctypes.byref(self.w), ctypes.byref(self.s))
         check()
 
     @property
     def persistent(self):
+        """The persistent step kernel is prepared (it runs the positions below
+        `s.step_switch_pos`)."""
         return bool(self.s.persistent)
+
+    def kernel_tokens(self, pos, n):
+        """How many of n tokens decoded from `pos` run in the persistent step kernel (one
+        launch); the others run one hipGraph replay each."""
+        if not self.s.persistent:
+            return 0
+        return max(0, min(n, self.s.step_switch_pos - pos))
+
+    def step_kind(self, pos, n):
+        k = self.kernel_tokens(pos, n)
+        if k == n:
+            return "persistent step kernel"
+        return "hipGraph of per-layer kernels" if k == 0 else \
+            f"persistent step kernel ({k} tokens), then hipGraph of per-layer kernels"
 
     def forward(self, token, pos):
         lib().forward(ctypes.byref(self.cfg), ctypes.byref(self.w), ctypes.byref(self.s), token,

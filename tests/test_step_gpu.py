@@ -462,6 +462,50 @@ def test_persistent_generate_one_launch_small(gpu, oracle):
         dec.close()
 
 
+def test_auto_step_switches_to_graph_at_switch_pos(gpu, oracle):
+    """STEP_AUTO prepares the persistent kernel for the positions below its switch position
+    (736 at hidden <= 1024) and the hipGraph from there on: single steps on either side of the
+    switch and one generate_greedy call that crosses it (36 tokens in the kernel's launch, 28
+    graph replays continuing from the token and position it left) equal the oracle, on the
+    smallest specialised shapes after a 700-position N(0, 1) cache."""
+    ident("auto step switch small shapes")
+    from llm_inference_amd import model
+    cfg = model.make_config(hidden_size=512, intermediate_size=1024, n_layers=3, n_heads=8,
+                            n_kv_heads=4, vocab_size=5000, max_seq_len=800)
+    dec = model.Decoder(cfg, ("synth", 6, 0.02, 0.1))
+    try:
+        rng = np.random.default_rng(736)
+        kvd = cfg.n_kv_heads * cfg.head_dim
+        k = np.zeros((cfg.n_layers, 800, kvd), np.uint16)
+        v = np.zeros_like(k)
+        k[:, :700] = rand_bf16(rng, (cfg.n_layers, 700, kvd))
+        v[:, :700] = rand_bf16(rng, (cfg.n_layers, 700, kvd))
+        dec.set_kv_cache(k, v)
+        w = dec.host_weights()
+        orc = oracle.Model(oracle_cfg(cfg), w, max_seq=800)
+        orc.bufs["key_cache"][:] = k.reshape(-1)
+        orc.bufs["value_cache"][:] = v.reshape(-1)
+        dec.capture_graph("auto")
+        assert dec.persistent and dec.s.step_switch_pos == 736
+        assert dec.kernel_tokens(700, 64) == 36
+        got = dec.generate_greedy(1234, 700, 64)
+        t, ref = 1234, []
+        for i in range(64):
+            t = orc.forward(t, 700 + i, oracle.GPU_ORDER)
+            ref.append(t)
+        assert got == ref
+        # single steps (rewriting a row as the oracle does): 735 in the kernel, 736 and 764 in
+        # the graph
+        for pos in (735, 736, 764):
+            dec.forward(77 + pos, pos)
+            nxt = dec.sample_argmax()
+            want = orc.forward(77 + pos, pos, oracle.GPU_ORDER)
+            assert np.array_equal(dec.logits(), orc.logits), pos
+            assert nxt == want, pos
+    finally:
+        dec.close()
+
+
 @pytest.mark.parametrize("size", ["1.7B", "4B"])
 def test_persistent_step_wide_shapes(gpu, oracle, size):
     """The Qwen3-1.7B and -4B specialisations of the persistent step (their widths and heads,
