@@ -1375,15 +1375,16 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
     static_assert(D % CC == 0, "columns per workgroup");
     __shared__ float part[CB * CC];
     const int h = blockIdx.x / (D / CC), c0 = (blockIdx.x % (D / CC)) * CC;
-    const int n = *a.d_pos + 1;
-    const int nb = (n + ATT_B - 1) / ATT_B;
     const float *src = a.partial + (size_t)h * a.max_blocks * D + c0;
     float acc = 0.0f;
-    for (int b0 = 0; b0 < nb; b0 += CB) {
-        const int cnt = min(CB, nb - b0);
+    // Each chunk's loads cover min(CB, max_blocks - b0) blocks, whatever the history, and the
+    // position is read after them (a per-lane load: as a uniform value it would be loaded, and
+    // waited for, before them): one round trip instead of two. Blocks past the history are
+    // loaded and not added.
+    for (int b0 = 0; b0 < a.max_blocks; b0 += CB) {
         if (b0 > 0) __syncthreads();  // the previous chunk has been added
         constexpr int PER = CB * Q / 256;  // 16-byte loads per thread for a full chunk
-        const int n4 = cnt * Q;
+        const int n4 = min(CB, a.max_blocks - b0) * Q;
         u32x4 v4[PER];
 #pragma unroll
         for (int j = 0; j < PER; j++) {
@@ -1391,9 +1392,14 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(AttnArgs a) {
             const int i = min((int)threadIdx.x + 256 * j, n4 - 1);
             v4[j] = *(const u32x4 *)(src + (size_t)(b0 + i / Q) * D + 4 * (i % Q));
         }
+        const int n = a.d_pos[tid_x() >> 31] + 1;
+        // staged before the history is looked at, so the loads above cannot be moved past it
 #pragma unroll
         for (int j = 0; j < PER; j++)
             if ((int)threadIdx.x + 256 * j < n4) ((u32x4 *)part)[threadIdx.x + 256 * j] = v4[j];
+        const int nb = __builtin_amdgcn_readfirstlane((n + ATT_B - 1) / ATT_B);
+        if (b0 >= nb) break;
+        const int cnt = min(CB, nb - b0);
         __syncthreads();
         if (threadIdx.x < CC) {
             // 16 LDS reads in flight, then their additions in order
