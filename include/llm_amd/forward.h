@@ -77,7 +77,7 @@ typedef struct {
     size_t gpu_bytes;
 } Weights;
 
-/* src/forward.cuh:6-25, plus the device state this build's step keeps after the reference's
+/* src/forward.cuh:6-25, plus the device state the gfx950 step keeps after the reference's
  * fields (attention workspace, argmax partials, the on-device token stream). */
 typedef struct {
     bf16 *x;

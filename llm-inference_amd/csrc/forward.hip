@@ -1,5 +1,5 @@
 // Decode step of the gfx950 build: run state, the per-layer launch order of the reference's
-// forward_kernels (src/forward.cu:118-193) on this build's kernels, hipGraph capture and replay,
+// forward_kernels (src/forward.cu:118-193) on the gfx950 kernels, hipGraph capture and replay,
 // greedy sampling, and a decode loop that stays on the device (argmax feeds the next step's
 // embedding, the position advances in a kernel, tokens are copied out once at the end).
 #include <math.h>

@@ -1,7 +1,7 @@
 /*
  * CPU oracle for the fused Qwen3 decode-layer path. TEST INFRASTRUCTURE ONLY: only tests/,
- * __graft_entry__.smoke() and bench.py's cpu_baseline leg load it, as the checker or as the
- * timed CPU baseline. Nothing in the product path links or calls it.
+ * __graft_entry__.smoke() and bench.py's cpu_baseline leg load it, as the results the GPU path
+ * is compared with or as the timed CPU baseline. Nothing in the product path links or calls it.
  *
  * What each function restates (reference = William-Lamer/llm-inference):
  *   orc_embedding      src/kernels.cu:7-15

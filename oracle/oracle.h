@@ -2,7 +2,7 @@
  * CPU oracle for the fused Qwen3 decode-layer path. TEST INFRASTRUCTURE ONLY.
  *
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may load this
- * library, and only as the checker (or the timed CPU baseline). The product path
+ * library, and only as the results the GPU path is compared with (or the timed CPU baseline). The product path
  * (llm-inference_amd/) never links, loads or calls it.
  *
  * It restates, in plain C on the CPU, the arithmetic of William-Lamer/llm-inference's

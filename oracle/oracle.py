@@ -1,7 +1,7 @@
 """ctypes wrapper of the CPU oracle (liboracle.so). TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this module, as the
-checker or as the timed CPU baseline; the product path never does. bf16 tensors are numpy
+results the GPU path is compared with or as the timed CPU baseline; the product path never does. bf16 tensors are numpy
 uint16 arrays of raw bits. ``mode`` is GPU_ORDER (bit-exact mirror of the HIP kernels'
 summation order) or EXACT (double accumulation, libm transcendentals).
 """

@@ -1,6 +1,6 @@
 """End-to-end decode on the GPU against the CPU oracle's whole-step restatement.
 
-The step (src/forward.cu:118-193 order, this build's kernels) must give logits bit-identical to
+The step (src/forward.cu:118-193 order, the gfx950 kernels) must give logits bit-identical to
 the oracle's GPU-order step at every position, eager and graph-replayed alike, and greedy
 sequences bit-identical over 32 (Qwen3-0.6B shapes) and 256 tokens. A small model goes through
 the safetensors loader so the loader's tensors, checksums and tied LM head are checked on the
