@@ -462,6 +462,45 @@ def test_persistent_generate_one_launch_small(gpu, oracle):
         dec.close()
 
 
+@pytest.mark.parametrize("head_dim,attn", [(64, "in_scores"), (64, "separate"),
+                                           (256, "in_scores"), (256, "separate")])
+def test_graph_step_other_head_dims(gpu, oracle, head_dim, attn):
+    """The hipGraph step at head_dim 64 and 256 (shapes with no persistent kernel: STEP_AUTO
+    captures the graph), in both attention forms: QK-norm + RoPE inside the scores pass reading
+    the step's RoPE table (rope_table_kernel), and qk_norm_rope_forward + attention_forward.
+    Logits bit-identical to the oracle at positions 0-69 (crossing the first 64-position block)
+    of a prompt fed one token at a time, then a 24-token generate_greedy equal to the
+    oracle's."""
+    ident(f"graph step head_dim {head_dim} {attn}")
+    from llm_inference_amd import model
+    cfg = model.make_config(hidden_size=512, intermediate_size=1024, n_layers=2, n_heads=8,
+                            n_kv_heads=4, head_dim=head_dim, vocab_size=3000, max_seq_len=128)
+    dec = model.Decoder(cfg, ("synth", head_dim, 0.02, 0.1))
+    try:
+        w = dec.host_weights()
+        orc = oracle.Model(oracle_cfg(cfg), w, max_seq=128)
+        dec.s.attn_mode = model.ATTN_MODES[attn]
+        dec.capture_graph("auto")
+        assert not dec.persistent
+        rng = np.random.default_rng(head_dim)
+        tok = 0
+        for pos in range(70):
+            tok = int(rng.integers(0, cfg.vocab_size))
+            dec.forward(tok, pos)
+            nxt = dec.sample_argmax()
+            ref = orc.forward(tok, pos, oracle.GPU_ORDER)
+            assert np.array_equal(dec.logits(), orc.logits), pos
+            assert nxt == ref, pos
+        got = dec.generate_greedy(nxt, 70, 24)
+        want, t = [], nxt
+        for i in range(24):
+            t = orc.forward(t, 70 + i, oracle.GPU_ORDER)
+            want.append(t)
+        assert got == want
+    finally:
+        dec.close()
+
+
 def test_auto_step_switches_to_graph_at_switch_pos(gpu, oracle):
     """STEP_AUTO prepares the persistent kernel for the positions below its switch position
     (736 at hidden <= 1024) and the hipGraph from there on: single steps on either side of the
