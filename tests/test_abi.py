@@ -379,3 +379,13 @@ def test_byte_counts_match_the_published_figures():
     H, I, D, qd, kvd = 64, 96, 16, 64, 32
     layer = H + qd * H + 2 * kvd * H + 2 * D + H * qd + H + 2 * I * H + H * I
     assert model.weight_bytes_per_step(c) == 2 * (3 * layer + H + 50 * H + H)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus N > 1 exits with status 2 and says why, before any GPU
+    or library work (the argument check comes first)."""
+    r = subprocess.run([sys.executable, str(Path(ROOT) / "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2
+    assert "--gpus 2 is not supported" in r.stderr
+    assert r.stdout == ""
