@@ -93,7 +93,7 @@ def bf16_step(b, k):
 
 
 def within_one_ulp_then_scale(y, n_exact, scale):
-    """True where y = bf16(m * scale) for some m within one bf16 ulp of n_exact: the north-star
+    """True where y = bf16(m * scale) for some m within one bf16 ulp of n_exact: the parity
     1-ulp tolerance applied at HF's first rounding point (bf16(x * inv_rms) for RMSNorm,
     bf16(silu(g)) for SwiGLU), followed by the same bf16 multiply by gamma (or up)."""
     y = np.asarray(y, dtype=np.uint16)

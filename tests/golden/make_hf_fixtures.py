@@ -15,7 +15,7 @@ the bench's 5 seeded prompt ids:
 
 These pin what no closed form does: the HF fp32/bf16 CPU arithmetic end to end (the e2e logits
 within 2e-2 and the greedy sequence up to near ties). The fixtures are data; this script is the
-only place transformers is imported, and only here (never on the GPU box).
+only place transformers is imported, and only here (never by the GPU tests or the bench).
 
 Run from the repository root:  python tests/golden/make_hf_fixtures.py [small] [dumps] [0.6B]
 """

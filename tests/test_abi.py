@@ -322,7 +322,7 @@ def test_load_weights_duplicate_across_shards(tmp_path):
 def test_load_weights_tied_head_may_be_present(tmp_path):
     """With tie_word_embeddings an lm_head.weight in the files is allowed (not read): a complete
     checkpoint passes every check and only then reaches the device (without a GPU the first HIP
-    call reports the error; on a GPU box the load succeeds)."""
+    call reports the error; on a machine with a GPU the load succeeds)."""
     t = _small_tensors()
     t["lm_head.weight"] = ("BF16", [1000, 256], 1000 * 256 * 2)
     msg = _load_error_or_none(tmp_path, t)

@@ -1,7 +1,7 @@
 """Parity of every HIP launcher with the CPU oracle on the same seeded inputs.
 
 GPU results must be bit-identical to the oracle's GPU-order mode (same fp32 operations in the
-same order) and within the north-star tolerance of its exact mode: 1 bf16 ulp for RMSNorm,
+same order) and within the parity tolerance of its exact mode: 1 bf16 ulp for RMSNorm,
 RoPE and SwiGLU, bit-exact for the embedding rows, KV-cache slots and argmax. Shapes are the
 Qwen3-0.6B decode layer (hidden 1024, 16q/8kv heads of 128, intermediate 3072, vocab 151936),
 the Qwen3-4B widths (2560, 32/8, 9728) and the many-row roofline sweep sizes, plus ragged and

@@ -374,7 +374,7 @@ def test_byte_counts_match_published(oracle):
 # ---------------------------------------------------------------- HF golden fixture
 
 HF_FIXTURE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "hf_small_qwen3.npz")
-LOGIT_TOL = 2e-2  # the north star's final-logits bound against the HF path
+LOGIT_TOL = 2e-2  # the final-logits bound against the HF path
 TIE_GAP = 0.25    # ref/compare.py:18: a greedy flip is accepted only below this top-2 gap
 
 

@@ -252,12 +252,12 @@ def test_qwen3_06b_greedy_256_vs_hf_fixture(gpu):
     greedy tokens after the bench's prompt), persistent step, teacher-forced on HF's tokens so
     every step sees HF's context: at all 256 steps the GPU's logits at HF's 8 largest indices are
     within 2 bf16 ulps of HF's, and wherever HF's top-2 gap exceeds 0.07 (more than the two
-    sides' combined error) the GPU's argmax is HF's token. Two ulps, not the north star's 2e-2:
+    sides' combined error) the GPU's argmax is HF's token. Two ulps, not the 2e-2 logit bound:
     after 28 layers of bf16 rounding, the oracle's exact-arithmetic mode (double accumulation,
     libm transcendentals) is itself 2 ulps (0.031 at |logit| ~2.7) from HF's CPU path at some of
     these steps, so no summation order meets 2e-2 everywhere. At the fixture's 9 full-vocabulary
     steps (0, 32, ..., 224, 255) every one of the 151936 logits is compared: the max-abs
-    difference is printed against the north star's 2e-2 (with the count of logits above it), and
+    difference is printed against the 2e-2 logit bound (with the count of logits above it), and
     every logit must be within 4 bf16 ulps, in units of the row's largest logit, of HF's value (a
     logit's error comes from the final hidden vector's, on the scale of the row). The oracle's
     exact mode, teacher-forced the same way, is itself 0.0518 (3.31 such ulps) from HF over these
@@ -311,7 +311,7 @@ def test_qwen3_06b_greedy_256_vs_hf_fixture(gpu):
         print(f"[case] max logit diff {worst:.4f}; argmax equal at {agree}/{decided} decided steps",
               flush=True)
         print(f"[case] all {f['full_logits'].shape[1]} logits at steps {full_steps}: max-abs "
-              f"{full_worst:.4f} (north-star bound 2e-2), {full_over} of "
+              f"{full_worst:.4f} (logit bound 2e-2), {full_over} of "
               f"{len(full_steps) * f['full_logits'].shape[1]} logits above 2e-2, at most "
               f"{full_ulps:.2f} bf16 ulps of the row's largest logit", flush=True)
         assert full_ulps <= 4, full_ulps
