@@ -1203,9 +1203,10 @@ struct Shape {
     static constexpr int B_GU = H <= 1024 ? 2 : 1;
     static constexpr int B_DOWN = 1;
     static constexpr int B_LM = H <= 2048 ? 4 : 2;  // 0.6B: 4 rows +0.4% over 8, 16 spills
-    // copies of x, the attention output and the SwiGLU output (at most STEP_REPLICAS):
-    // 0.6B 8 (4: -0.2%, 16: -2.6%), 1.7B 4 (+4.2% over 8)
-    static constexpr int REPLICAS = H <= 1024 ? 8 : 4;
+    // copies of x, the attention output and the SwiGLU output (at most STEP_REPLICAS), each
+    // 1 KB off the 4 KB grid (step_replica_stride): 4 at every shape (0.6B: 2291-2294 tokens/s
+    // against 2280-2282 with 8, on two boxes; 1.7B: 1115 against 1074)
+    static constexpr int REPLICAS = 4;
     // 1.7B: the down rows with attention 1050 -> 1075 tokens/s, the q/k/v rows too 1005
     static constexpr int PF_D = H <= 2048 ? PF_WITH_ATTENTION : PF_AFTER_COMPUTE;
     static constexpr int PF_QKV = H <= 1024 ? PF_WITH_ATTENTION : PF_AFTER_COMPUTE;
