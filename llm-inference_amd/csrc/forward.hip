@@ -23,6 +23,19 @@ static bool dmalloc(void **p, size_t bytes) {
     return HIP_OK(hipMemset(*p, 0, bytes));
 }
 
+// The attention workspace's bytes, rounded up to 256.
+static size_t att_bytes(const Config *cfg, int max_seq) {
+    return (attention_workspace_floats(cfg->n_heads, cfg->head_dim, max_seq) * 4 + 255) / 256 * 256;
+}
+
+// The workspace of the one-launch PV and combine inside RunState::att, or NULL where the shapes
+// do not take it.
+static void *pvc_workspace(const Config *cfg, const RunState *s) {
+    if (!attention_pv_combine_bytes(cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, s->max_seq))
+        return nullptr;
+    return (char *)s->att + att_bytes(cfg, s->max_seq);
+}
+
 extern "C" void alloc_run_state_seq(RunState *s, const Config *cfg, int max_seq) {
     memset(s, 0, sizeof *s);
     if (max_seq <= 0) {
@@ -37,11 +50,15 @@ extern "C" void alloc_run_state_seq(RunState *s, const Config *cfg, int max_seq)
     size_t tap_len = q_dim;
     if (I > tap_len) tap_len = I;
     if (H > tap_len) tap_len = H;
-    const size_t att = attention_workspace_floats(cfg->n_heads, cfg->head_dim, max_seq);
+    // `att` holds the attention workspace, then (from a 256-byte boundary) the workspace of the
+    // one-launch PV and combine where the shapes take it
+    const size_t att = att_bytes(cfg, max_seq) +
+                       attention_pv_combine_bytes(cfg->n_heads, cfg->n_kv_heads, cfg->head_dim,
+                                                  max_seq);
     bool ok = dmalloc((void **)&s->x, H * 2) && dmalloc((void **)&s->xb, H * 2) &&
               dmalloc((void **)&s->q, q_dim * 2) && dmalloc((void **)&s->k, kv_dim * 2) &&
               dmalloc((void **)&s->v, kv_dim * 2) && dmalloc((void **)&s->attn_out, q_dim * 2) &&
-              dmalloc((void **)&s->att, att * 4) && dmalloc((void **)&s->key_cache, cache_len * 2) &&
+              dmalloc((void **)&s->att, att) && dmalloc((void **)&s->key_cache, cache_len * 2) &&
               dmalloc((void **)&s->value_cache, cache_len * 2) && dmalloc((void **)&s->hb, I * 2) &&
               dmalloc((void **)&s->tap1, tap_len * 2) && dmalloc((void **)&s->tap2, tap_len * 2) &&
               dmalloc((void **)&s->logits, (size_t)cfg->vocab_size * 2) &&
@@ -127,6 +144,9 @@ static bool forward_kernels(const Config *cfg, const Weights *w, RunState *s) {
         (s->attn_mode == ATTN_IN_SCORES ||
          (s->attn_mode == ATTN_AUTO && (attn_items <= 256 || (D <= 128 && rep <= 4))));
     bf16 *tap1 = dumping ? s->tap1 : nullptr, *tap2 = dumping ? s->tap2 : nullptr;
+    // PV and combine as one launch (attn_pv_combine_kernel, the same bits) where the shapes
+    // take it
+    void *pvc = pvc_workspace(cfg, s);
     embedding_checked(s->x, w->embed, s->next_token, H, cfg->vocab_size, s->error_flag, st);
     dump_bf16("embed", s->x, H);
     // The in-scores attention of every layer reads the RoPE table of this position from one
@@ -158,7 +178,7 @@ static bool forward_kernels(const Config *cfg, const Weights *w, RunState *s) {
             qk_norm_rope_attention_launch(s->attn_out, s->q, s->k, s->v, L->q_norm, L->k_norm, kc,
                                           vc, s->att, s->pos, cfg->n_heads, cfg->n_kv_heads, D,
                                           cfg->rms_norm_eps, cfg->rope_theta, s->max_seq, scale,
-                                          st, s->rope_table);
+                                          st, s->rope_table, pvc, s->error_flag);
         } else {
             qk_norm_rope_forward(s->q, s->k, s->v, L->q_norm, L->k_norm, kc, vc, s->pos,
                                  cfg->n_heads, cfg->n_kv_heads, D, cfg->rms_norm_eps,
@@ -167,8 +187,8 @@ static bool forward_kernels(const Config *cfg, const Weights *w, RunState *s) {
             dump_layer(l, "k_norm", tap2, kv_dim);
             dump_layer(l, "q_rope", s->q, q_dim);
             dump_layer(l, "k_rope", s->k, kv_dim);
-            attention_forward(s->attn_out, s->q, kc, vc, s->att, cfg->n_heads, cfg->n_kv_heads, D,
-                              s->pos, s->max_seq, scale, st);
+            attention_launch(s->attn_out, s->q, kc, vc, s->att, cfg->n_heads, cfg->n_kv_heads, D,
+                             s->pos, s->max_seq, scale, st, pvc, s->error_flag);
         }
         dump_layer(l, "attn_out", s->attn_out, q_dim);
         gemv_residual_forward(s->x, L->wo, s->attn_out, H, q_dim, tap1, st);

@@ -1212,153 +1212,164 @@ void attn_rope_scores_kernel(AttnRopeArgs r) {
 // statistics: tree sum of S_b exp(m_b - M), chunks added in order), the block's probabilities
 // p = bf16(exp(s - M) / sum), then p v accumulated per lane over its positions, tree over the
 // position groups of a wave, waves added in order 0..3.
-template <int D, int REP>
-__global__ __launch_bounds__(256) void attn_pv_kernel(AttnArgs a) {
+// One item of pass 2, block b of kv head g: the probabilities of the block's positions for the
+// REP query heads, and the block's partial output sum p v of each head, handed over as
+// store(index into the [n_heads, max_blocks, D] partials, value).
+template <int D, int REP, class Store>
+__device__ __forceinline__ void pv_item(const AttnArgs &a, int b, int g, int n, int nb,
+                                        float (&p_s)[REP][ATT_B], float (&red)[4][REP][D],
+                                        Store store) {
     constexpr int LP = D / 8, PPW = 64 / LP, PER_WAVE = ATT_B / 4, ITERS = PER_WAVE / PPW;
-    __shared__ float p_s[REP][ATT_B];
-    __shared__ float red[4][REP][D];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int G = lane / LP, L = lane % LP;
-    const int n = *a.d_pos + 1;
-    const int nb = (n + ATT_B - 1) / ATT_B;
     const int kv_dim = a.n_kv_heads * D;
-    for (int item = blockIdx.x; item < nb * a.n_kv_heads; item += gridDim.x) {
-        const int b = item / a.n_kv_heads, g = item - b * a.n_kv_heads;
-        // The first head of this wave (r = w): its score and block statistics are requested
-        // before the values. Loads complete in order, so the statistics chain then waits only
-        // for them and runs while the values stream. Unconditional (clamped indices), so no
-        // branch joins before the value requests.
-        constexpr int MAXC = 4;  // chunks of 64 block statistics held in registers
-        const int r_first = w < REP ? w : 0;
-        float mv0[MAXC], sv0[MAXC], s_t0;
-        {
-            const int h = g * REP + r_first;
-            const float *st = a.stats + (size_t)h * a.max_blocks * 2;
-            s_t0 = a.scores[(size_t)h * a.max_seq + min(b * ATT_B + lane, n - 1)];
+    // The first head of this wave (r = w): its score and block statistics are requested
+    // before the values. Loads complete in order, so the statistics chain then waits only
+    // for them and runs while the values stream. Unconditional (clamped indices), so no
+    // branch joins before the value requests.
+    constexpr int MAXC = 4;  // chunks of 64 block statistics held in registers
+    const int r_first = w < REP ? w : 0;
+    float mv0[MAXC], sv0[MAXC], s_t0;
+    {
+        const int h = g * REP + r_first;
+        const float *st = a.stats + (size_t)h * a.max_blocks * 2;
+        s_t0 = a.scores[(size_t)h * a.max_seq + min(b * ATT_B + lane, n - 1)];
+#pragma unroll
+        for (int c = 0; c < MAXC; c++) {
+            const int bi = min(c * 64 + lane, nb - 1);
+            mv0[c] = st[2 * bi];
+            sv0[c] = st[2 * bi + 1];
+        }
+    }
+    // every lane requests a value row (positions past n clamped to n - 1: the PV loop skips
+    // those slots), so no load sits on some paths only and no wait is made conservative
+    u32x4 vv[ITERS];
+#pragma unroll
+    for (int it = 0; it < ITERS; it++) {
+        const int t = min(b * ATT_B + w * PER_WAVE + it * PPW + G, n - 1);
+        vv[it] = ld16_nt(a.vc + (size_t)t * kv_dim + g * D + 8 * L);
+    }
+    // The first head's probabilities from those statistics (nb <= 64 * MAXC: the max is exact
+    // in any order, so over the lane's chunks first and then one wave_max; the chunk sums
+    // added in order), computed by every wave with no branch, so the requests above are not
+    // moved below the value requests. Kept only by a wave that has a head, for nb <= 64 MAXC.
+    float p0;
+    {
+        float ml = -__builtin_huge_valf();
+#pragma unroll
+        for (int c = 0; c < MAXC; c++) ml = c * 64 + lane < nb ? fmaxf(ml, mv0[c]) : ml;
+        const float M = wave_max(ml);
+        float cs[MAXC];
+#pragma unroll
+        for (int c = 0; c < MAXC; c++)
+            cs[c] = wave_sum(c * 64 + lane < nb ? sv0[c] * exp_f32(mv0[c] - M) : 0.0f);
+        float sum = cs[0];
+#pragma unroll
+        for (int c = 1; c < MAXC; c++) sum = c * 64 < nb ? sum + cs[c] : sum;
+        p0 = b * ATT_B + lane < n ? round_bf(exp_f32(s_t0 - M) / sum) : 0.0f;
+    }
+    for (int r = w; r < REP; r += 4) {
+        if (r == w && nb <= 64 * MAXC) {
+            p_s[r][lane] = p0;
+            continue;
+        }
+        // a second head of the wave (REP = 8), or more than 64 * MAXC blocks
+        const int h = g * REP + r;
+        const float *st = a.stats + (size_t)h * a.max_blocks * 2;
+        const int t = b * ATT_B + lane;
+        const float s_t = a.scores[(size_t)h * a.max_seq + min(t, n - 1)];
+        float M = -__builtin_huge_valf(), sum = 0.0f;
+        if (nb <= 64 * MAXC) {
+            // every statistic requested at once (clamped indices, no branch around the
+            // loads), then the same max and in-order chunk sums as p0's
+            float mv[MAXC], sv[MAXC];
 #pragma unroll
             for (int c = 0; c < MAXC; c++) {
                 const int bi = min(c * 64 + lane, nb - 1);
-                mv0[c] = st[2 * bi];
-                sv0[c] = st[2 * bi + 1];
+                mv[c] = st[2 * bi];
+                sv[c] = st[2 * bi + 1];
             }
-        }
-        // every lane requests a value row (positions past n clamped to n - 1: the PV loop skips
-        // those slots), so no load sits on some paths only and no wait is made conservative
-        u32x4 vv[ITERS];
-#pragma unroll
-        for (int it = 0; it < ITERS; it++) {
-            const int t = min(b * ATT_B + w * PER_WAVE + it * PPW + G, n - 1);
-            vv[it] = ld16_nt(a.vc + (size_t)t * kv_dim + g * D + 8 * L);
-        }
-        // The first head's probabilities from those statistics (nb <= 64 * MAXC: the max is exact
-        // in any order, so over the lane's chunks first and then one wave_max; the chunk sums
-        // added in order), computed by every wave with no branch, so the requests above are not
-        // moved below the value requests. Kept only by a wave that has a head, for nb <= 64 MAXC.
-        float p0;
-        {
             float ml = -__builtin_huge_valf();
 #pragma unroll
-            for (int c = 0; c < MAXC; c++) ml = c * 64 + lane < nb ? fmaxf(ml, mv0[c]) : ml;
-            const float M = wave_max(ml);
-            float cs[MAXC];
+            for (int c = 0; c < MAXC; c++)
+                if (c * 64 + lane < nb) ml = fmaxf(ml, mv[c]);
+            M = wave_max(ml);
 #pragma unroll
             for (int c = 0; c < MAXC; c++)
-                cs[c] = wave_sum(c * 64 + lane < nb ? sv0[c] * exp_f32(mv0[c] - M) : 0.0f);
-            float sum = cs[0];
-#pragma unroll
-            for (int c = 1; c < MAXC; c++) sum = c * 64 < nb ? sum + cs[c] : sum;
-            p0 = b * ATT_B + lane < n ? round_bf(exp_f32(s_t0 - M) / sum) : 0.0f;
-        }
-        for (int r = w; r < REP; r += 4) {
-            if (r == w && nb <= 64 * MAXC) {
-                p_s[r][lane] = p0;
-                continue;
-            }
-            // a second head of the wave (REP = 8), or more than 64 * MAXC blocks
-            const int h = g * REP + r;
-            const float *st = a.stats + (size_t)h * a.max_blocks * 2;
-            const int t = b * ATT_B + lane;
-            const float s_t = a.scores[(size_t)h * a.max_seq + min(t, n - 1)];
-            float M = -__builtin_huge_valf(), sum = 0.0f;
-            if (nb <= 64 * MAXC) {
-                // every statistic requested at once (clamped indices, no branch around the
-                // loads), then the same max and in-order chunk sums as p0's
-                float mv[MAXC], sv[MAXC];
-#pragma unroll
-                for (int c = 0; c < MAXC; c++) {
-                    const int bi = min(c * 64 + lane, nb - 1);
-                    mv[c] = st[2 * bi];
-                    sv[c] = st[2 * bi + 1];
-                }
-                float ml = -__builtin_huge_valf();
-#pragma unroll
-                for (int c = 0; c < MAXC; c++)
-                    if (c * 64 + lane < nb) ml = fmaxf(ml, mv[c]);
-                M = wave_max(ml);
-#pragma unroll
-                for (int c = 0; c < MAXC; c++)
-                    if (c * 64 < nb) {
-                        const float term = c * 64 + lane < nb ? sv[c] * exp_f32(mv[c] - M) : 0.0f;
-                        const float cs = wave_sum(term);
-                        sum = c == 0 ? cs : sum + cs;
-                    }
-            } else {
-                for (int c0 = 0; c0 < nb; c0 += 64) {
-                    const int bi = c0 + lane;
-                    M = fmaxf(M, wave_max(bi < nb ? st[2 * bi] : -__builtin_huge_valf()));
-                }
-                for (int c0 = 0; c0 < nb; c0 += 64) {
-                    const int bi = c0 + lane;
-                    const float term = bi < nb ? st[2 * bi + 1] * exp_f32(st[2 * bi] - M) : 0.0f;
+                if (c * 64 < nb) {
+                    const float term = c * 64 + lane < nb ? sv[c] * exp_f32(mv[c] - M) : 0.0f;
                     const float cs = wave_sum(term);
-                    sum = c0 == 0 ? cs : sum + cs;
+                    sum = c == 0 ? cs : sum + cs;
                 }
+        } else {
+            for (int c0 = 0; c0 < nb; c0 += 64) {
+                const int bi = c0 + lane;
+                M = fmaxf(M, wave_max(bi < nb ? st[2 * bi] : -__builtin_huge_valf()));
             }
-            p_s[r][lane] = t < n ? round_bf(exp_f32(s_t - M) / sum) : 0.0f;
-        }
-        __syncthreads();
-        float acc[REP][8];
-#pragma unroll
-        for (int r = 0; r < REP; r++)
-#pragma unroll
-            for (int e = 0; e < 8; e++) acc[r][e] = 0.0f;
-#pragma unroll
-        for (int it = 0; it < ITERS; it++) {
-            const int slot = w * PER_WAVE + it * PPW + G;
-            if (b * ATT_B + slot < n) {
-#pragma unroll
-                for (int r = 0; r < REP; r++) {
-                    const float p = p_s[r][slot];
-#pragma unroll
-                    for (int e = 0; e < 8; e++) acc[r][e] = fmaf(p, elem(vv[it], e), acc[r][e]);
-                }
+            for (int c0 = 0; c0 < nb; c0 += 64) {
+                const int bi = c0 + lane;
+                const float term = bi < nb ? st[2 * bi + 1] * exp_f32(st[2 * bi] - M) : 0.0f;
+                const float cs = wave_sum(term);
+                sum = c0 == 0 ? cs : sum + cs;
             }
         }
-        // the position groups (lanes LP apart) summed with the pairing of butterfly_sum<LP, 64>,
-        // reduce-scattered: each lane keeps REP * 8 / (64 / LP) of the values, at offset `off`
-        constexpr int NV = REP * 8, NG = 64 / LP, KEEP = NV / NG;
-        float flat[NV], kept[KEEP];
+        p_s[r][lane] = t < n ? round_bf(exp_f32(s_t - M) / sum) : 0.0f;
+    }
+    __syncthreads();
+    float acc[REP][8];
 #pragma unroll
-        for (int r = 0; r < REP; r++)
+    for (int r = 0; r < REP; r++)
 #pragma unroll
-            for (int e = 0; e < 8; e++) flat[r * 8 + e] = acc[r][e];
-        scatter_keep<NV, LP, 64>(flat, kept);
-        int off = 0;
+        for (int e = 0; e < 8; e++) acc[r][e] = 0.0f;
 #pragma unroll
-        for (int k = 0, m = NV; (LP << k) < 64; k++, m >>= 1)
-            if ((lane >> k) & LP) off += m / 2;
+    for (int it = 0; it < ITERS; it++) {
+        const int slot = w * PER_WAVE + it * PPW + G;
+        if (b * ATT_B + slot < n) {
 #pragma unroll
-        for (int j = 0; j < KEEP; j++) {
-            const int idx = off + j, r = idx / 8, e = idx % 8;
-            red[w][r][8 * L + e] = kept[j];
+            for (int r = 0; r < REP; r++) {
+                const float p = p_s[r][slot];
+#pragma unroll
+                for (int e = 0; e < 8; e++) acc[r][e] = fmaf(p, elem(vv[it], e), acc[r][e]);
+            }
         }
-        __syncthreads();
-        for (int i = threadIdx.x; i < REP * D; i += 256) {
-            const int r = i / D, d = i - r * D;
-            const float v = ((red[0][r][d] + red[1][r][d]) + red[2][r][d]) + red[3][r][d];
-            a.partial[((size_t)(g * REP + r) * a.max_blocks + b) * D + d] = v;
-        }
-        __syncthreads();
+    }
+    // the position groups (lanes LP apart) summed with the pairing of butterfly_sum<LP, 64>,
+    // reduce-scattered: each lane keeps REP * 8 / (64 / LP) of the values, at offset `off`
+    constexpr int NV = REP * 8, NG = 64 / LP, KEEP = NV / NG;
+    float flat[NV], kept[KEEP];
+#pragma unroll
+    for (int r = 0; r < REP; r++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) flat[r * 8 + e] = acc[r][e];
+    scatter_keep<NV, LP, 64>(flat, kept);
+    int off = 0;
+#pragma unroll
+    for (int k = 0, m = NV; (LP << k) < 64; k++, m >>= 1)
+        if ((lane >> k) & LP) off += m / 2;
+#pragma unroll
+    for (int j = 0; j < KEEP; j++) {
+        const int idx = off + j, r = idx / 8, e = idx % 8;
+        red[w][r][8 * L + e] = kept[j];
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < REP * D; i += 256) {
+        const int r = i / D, d = i - r * D;
+        const float v = ((red[0][r][d] + red[1][r][d]) + red[2][r][d]) + red[3][r][d];
+        store(((size_t)(g * REP + r) * a.max_blocks + b) * D + d, v);
+    }
+    __syncthreads();
+}
+
+template <int D, int REP>
+__global__ __launch_bounds__(256) void attn_pv_kernel(AttnArgs a) {
+    __shared__ float p_s[REP][ATT_B];
+    __shared__ float red[4][REP][D];
+    const int n = *a.d_pos + 1;
+    const int nb = (n + ATT_B - 1) / ATT_B;
+    for (int item = blockIdx.x; item < nb * a.n_kv_heads; item += gridDim.x) {
+        const int b = item / a.n_kv_heads, g = item - b * a.n_kv_heads;
+        pv_item<D, REP>(a, b, g, n, nb, p_s, red,
+                        [&](size_t i, float v) { a.partial[i] = v; });
     }
 }
 
@@ -1466,20 +1477,20 @@ __device__ __forceinline__ void op_st(unsigned long long *p, float v, uint32_t t
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Polls the tagged words addr(idx), idx = threadIdx.x + OP_THREADS k < total, until every tag
-// is `tag`, and hands each value to put(idx, value). Bounded: on timeout, or once another
-// workgroup has timed out, it sets *err and goes on with what it read.
-template <class Addr, class Put>
+// Polls the tagged words addr(idx), idx = threadIdx.x + NT k < total (NT threads in the
+// workgroup, K words of a thread in flight), until every tag is `tag`, and hands each value to
+// put(idx, value). Bounded: on timeout, or once another workgroup has timed out, it sets *err and
+// goes on with what it read.
+template <int NT = OP_THREADS, int K = 8, class Addr, class Put>
 __device__ __forceinline__ void op_poll(int total, uint32_t tag, int *err, Addr addr, Put put) {
-    constexpr int K = 8;
-    for (int base = 0; base < total; base += OP_THREADS * K) {
+    for (int base = 0; base < total; base += NT * K) {
         unsigned long long wv[K];
         long long spins = 0;
         for (;;) {
             bool fresh = true;
 #pragma unroll
             for (int k = 0; k < K; k++) {
-                const int idx = base + (int)threadIdx.x + OP_THREADS * k;
+                const int idx = base + (int)threadIdx.x + NT * k;
                 wv[k] = idx < total ? op_ld(addr(idx)) : 0ull;
                 fresh &= idx >= total || (uint32_t)wv[k] == tag;
             }
@@ -1493,7 +1504,7 @@ __device__ __forceinline__ void op_poll(int total, uint32_t tag, int *err, Addr 
         }
 #pragma unroll
         for (int k = 0; k < K; k++) {
-            const int idx = base + (int)threadIdx.x + OP_THREADS * k;
+            const int idx = base + (int)threadIdx.x + NT * k;
             if (idx < total) put(idx, __uint_as_float((uint32_t)(wv[k] >> 32)));
         }
     }
@@ -1956,9 +1967,118 @@ extern "C" void qk_norm_rope_attention_one_pass(bf16 *out, const bf16 *q, const 
                               stream);
 }
 
+// ------------------------------------------------------------------------------------------
+// Passes 2 and 3 in one launch (attn_pv_kernel followed by attn_combine_kernel, the same bits),
+// for the step's attention. Every item publishes its block partials as tagged 64-bit words
+// (float bits << 32 | tag; the tag is the workgroup's launch count + 1, counted in a word of
+// its own as in the one-pass kernel), and the items of the T last blocks of each kv head then
+// combine: item nb - T + j adds, in block order, the partials of columns [j C, (j + 1) C) of the
+// kv head's REP * D (C = REP * D / T), once it has read every block's partial of them with the
+// current tag. T is the largest power of two <= min(nb, REP * D / PVC_COLS). One workgroup per
+// item of the longest history, so the items of a step are one wave of the grid; only the
+// T * n_kv_heads combine items wait, every other item runs to its end, so the waits end. They
+// are bounded all the same: a timeout sets *err, and the kernel finishes with what it read.
+// ------------------------------------------------------------------------------------------
+
+constexpr int PVC_COLS = 16;        // fewest columns of a combine item
+constexpr int PVC_STRIDE = 16;      // 8-byte words between two workgroups' launch counters
+constexpr int PVC_MAXGRID = 8192;   // items (blocks x kv heads) of the longest history
+
+struct PvCombineArgs {
+    AttnArgs a;
+    unsigned long long *tpart;     // [n_heads, max_blocks, D] tagged block partials
+    unsigned long long *launches;  // per workgroup, PVC_STRIDE words apart: its launches
+    int *err;                      // set to 2 when a wait times out
+};
+
+template <int D, int REP>
+__global__ __launch_bounds__(256) void attn_pv_combine_kernel(PvCombineArgs o) {
+    constexpr int COLS = REP * D;
+    constexpr int STAGE = 4 * REP * D > 4096 ? 4 * REP * D : 4096;  // floats
+    constexpr int CPT = (COLS + 255) / 256;  // columns of a thread when one item combines all
+    __shared__ float p_s[REP][ATT_B];
+    __shared__ float stage[STAGE];  // the PV quarter sums, then the combine's staged partials
+    float(&red)[4][REP][D] = *reinterpret_cast<float(*)[4][REP][D]>(stage);
+    const AttnArgs &a = o.a;
+    unsigned long long *ctr = o.launches + (size_t)blockIdx.x * PVC_STRIDE;
+    const unsigned long long launches = op_ld(ctr);
+    const uint32_t tag = (uint32_t)(launches % 0xffffffffull) + 1u;
+    const int n = *a.d_pos + 1;
+    const int nb = (n + ATT_B - 1) / ATT_B;
+    if ((int)blockIdx.x < nb * a.n_kv_heads) {  // the grid holds every item: one each
+        const int b = blockIdx.x / a.n_kv_heads, g = blockIdx.x - b * a.n_kv_heads;
+        pv_item<D, REP>(a, b, g, n, nb, p_s, red,
+                        [&](size_t i, float v) { op_st(o.tpart + i, v, tag); });
+        int T = 1;
+        while (2 * T <= nb && 2 * T * PVC_COLS <= COLS) T *= 2;
+        if (b >= nb - T) {
+            const int nc = COLS / T, c0 = (b - (nb - T)) * nc;
+            const int cb = STAGE / nc;  // blocks per staged chunk
+            float acc[CPT];
+#pragma unroll
+            for (int k = 0; k < CPT; k++) acc[k] = 0.0f;
+            for (int b0 = 0; b0 < nb; b0 += cb) {
+                const int cnt = min(cb, nb - b0);
+                op_poll<256, 16>(
+                    cnt * nc, tag, o.err,
+                    [&](int idx) {
+                        const int bb = idx / nc, c = c0 + idx - bb * nc, q = c / D, d = c - q * D;
+                        return o.tpart + ((size_t)(g * REP + q) * a.max_blocks + b0 + bb) * D + d;
+                    },
+                    [&](int idx, float v) { stage[idx] = v; });
+                __syncthreads();
+#pragma unroll
+                for (int k = 0; k < CPT; k++) {
+                    const int c = threadIdx.x + 256 * k;
+                    if (c < nc) {
+                        int j0 = 0;
+                        if (b0 == 0) {
+                            acc[k] = stage[c];
+                            j0 = 1;
+                        }
+                        for (; j0 + 16 <= cnt; j0 += 16) {  // 16 LDS reads in flight, then adds
+                            float v[16];
+#pragma unroll
+                            for (int u = 0; u < 16; u++) v[u] = stage[(j0 + u) * nc + c];
+#pragma unroll
+                            for (int u = 0; u < 16; u++) acc[k] += v[u];
+                        }
+                        for (; j0 < cnt; j0++) acc[k] += stage[j0 * nc + c];
+                    }
+                }
+                __syncthreads();
+            }
+#pragma unroll
+            for (int k = 0; k < CPT; k++) {
+                const int c = c0 + threadIdx.x + 256 * k, q = c / D, d = c - q * D;
+                if ((int)threadIdx.x + 256 * k < nc)
+                    a.out[(size_t)(g * REP + q) * D + d] = (bf16)f2bf(acc[k]);
+            }
+        }
+    }
+    __syncthreads();  // every wave has its tag
+    if (threadIdx.x == 0)
+        __hip_atomic_store(gptr(ctr), launches + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Bytes of the attn_pv_combine_kernel workspace (the launch counters, then the tagged partials),
+// or 0 where that kernel is not used: head_dim other than 128, or more than PVC_MAXGRID items.
+size_t attention_pv_combine_bytes(int n_heads, int n_kv_heads, int head_dim, int max_seq) {
+    if (head_dim != 128 || n_kv_heads <= 0 || n_heads % n_kv_heads != 0 || max_seq <= 0) return 0;
+    const int rep = n_heads / n_kv_heads;
+    if (rep != 1 && rep != 2 && rep != 4 && rep != 8) return 0;
+    const size_t mb = ceil_div((size_t)max_seq, ATT_B);
+    if (mb * n_kv_heads > PVC_MAXGRID) return 0;
+    return mb * n_kv_heads * PVC_STRIDE * 8 + (size_t)n_heads * mb * head_dim * 8;
+}
+
+// The second and third passes: attn_pv_combine_kernel on the workspace `pvc` where given (grid
+// = every item of the longest history, as attention_pv_combine_bytes admits), else the PV and
+// combine kernels.
 template <int D, int REP>
 static void launch_attention_t(const AttnArgs &a, int grid, hipStream_t stream,
-                               const AttnRopeArgs *rope = nullptr) {
+                               const AttnRopeArgs *rope = nullptr, void *pvc = nullptr,
+                               int *err = nullptr) {
     if (rope && rope->table)
         attn_rope_scores_kernel<D, REP, true><<<grid, 256, 0, stream>>>(*rope);
     else if (rope)
@@ -1966,6 +2086,18 @@ static void launch_attention_t(const AttnArgs &a, int grid, hipStream_t stream,
     else
         attn_scores_kernel<D, REP><<<grid, 256, 0, stream>>>(a);
     if (!LAUNCH_OK()) return;
+    if constexpr (D == 128) {
+        if (pvc) {
+            PvCombineArgs o;
+            o.a = a;
+            o.launches = (unsigned long long *)pvc;
+            o.tpart = o.launches + (size_t)grid * PVC_STRIDE;
+            o.err = err;
+            attn_pv_combine_kernel<D, REP><<<grid, 256, 0, stream>>>(o);
+            LAUNCH_OK();
+            return;
+        }
+    }
     attn_pv_kernel<D, REP><<<grid, 256, 0, stream>>>(a);
     if (!LAUNCH_OK()) return;
     attn_combine_kernel<D><<<a.n_heads * (D / COMBINE_COLS), 256, 0, stream>>>(a);
@@ -2029,24 +2161,34 @@ static bool attention_args(AttnArgs &a, int &grid, bf16 *out, const bf16 *q,
     return true;
 }
 
-extern "C" void attention_forward(bf16 *out, const bf16 *q, const bf16 *key_cache,
-                                  const bf16 *value_cache, float *att, int n_heads, int n_kv_heads,
-                                  int head_dim, const int *d_pos, int max_seq, float scale,
-                                  hipStream_t stream) {
+bool attention_launch(bf16 *out, const bf16 *q, const bf16 *key_cache, const bf16 *value_cache,
+                      float *att, int n_heads, int n_kv_heads, int head_dim, const int *d_pos,
+                      int max_seq, float scale, hipStream_t stream, void *pvc, int *err) {
     AttnArgs a;
     int grid = 0;
     if (!attention_args(a, grid, out, q, key_cache, value_cache, att, n_heads, n_kv_heads,
                         head_dim, d_pos, max_seq, scale))
-        return;
+        return false;
+    if (pvc && (!err || !attention_pv_combine_bytes(n_heads, n_kv_heads, head_dim, max_seq)))
+        return llm_fail("attention: no one-launch PV and combine for these shapes");
     const int rep = n_heads / n_kv_heads;
-#define ATT(D_, R_)                                    \
-    if (head_dim == D_ && rep == R_) {                 \
-        launch_attention_t<D_, R_>(a, grid, stream);   \
-        return;                                        \
+#define ATT(D_, R_)                                                        \
+    if (head_dim == D_ && rep == R_) {                                     \
+        launch_attention_t<D_, R_>(a, grid, stream, nullptr, pvc, err);    \
+        return !llm_has_error();                                           \
     }
     ATT(64, 1) ATT(64, 2) ATT(64, 4) ATT(64, 8) ATT(128, 1) ATT(128, 2) ATT(128, 4) ATT(128, 8)
     ATT(256, 1) ATT(256, 2) ATT(256, 4) ATT(256, 8)
 #undef ATT
+    return false;
+}
+
+extern "C" void attention_forward(bf16 *out, const bf16 *q, const bf16 *key_cache,
+                                  const bf16 *value_cache, float *att, int n_heads, int n_kv_heads,
+                                  int head_dim, const int *d_pos, int max_seq, float scale,
+                                  hipStream_t stream) {
+    attention_launch(out, q, key_cache, value_cache, att, n_heads, n_kv_heads, head_dim, d_pos,
+                     max_seq, scale, stream, nullptr, nullptr);
 }
 
 // Workspace of attention_forward_noalloc: a library-owned device array instead of the caller's
@@ -2083,13 +2225,15 @@ bool qk_norm_rope_attention_launch(bf16 *out, const bf16 *q, const bf16 *k, cons
                                    bf16 *value_cache, float *att, const int *d_pos, int n_heads,
                                    int n_kv_heads, int head_dim, float eps, float theta,
                                    int max_seq, float scale, hipStream_t stream,
-                                   const float *rope_table) {
+                                   const float *rope_table, void *pvc, int *err) {
     AttnRopeArgs r;
     memset(&r, 0, sizeof r);
     int grid = 0;
     if (!attention_args(r.at, grid, out, q, key_cache, value_cache, att, n_heads, n_kv_heads,
                         head_dim, d_pos, max_seq, scale))
         return false;
+    if (pvc && (!err || !attention_pv_combine_bytes(n_heads, n_kv_heads, head_dim, max_seq)))
+        return llm_fail("qk_norm_rope_attention: no one-launch PV and combine for these shapes");
     const void *ptrs[] = {k, v, q_norm_w, k_norm_w};
     for (const void *p : ptrs)
         if (!p || !aligned16(p))
@@ -2107,8 +2251,8 @@ bool qk_norm_rope_attention_launch(bf16 *out, const bf16 *q, const bf16 *k, cons
     const int rep = n_heads / n_kv_heads;
 #define ATT(D_, R_)                                        \
     if (head_dim == D_ && rep == R_) {                     \
-        launch_attention_t<D_, R_>(r.at, grid, stream, &r);\
-        return !llm_has_error();                           \
+        launch_attention_t<D_, R_>(r.at, grid, stream, &r, pvc, err);\
+        return !llm_has_error();                                     \
     }
     ATT(64, 1) ATT(64, 2) ATT(64, 4) ATT(64, 8) ATT(128, 1) ATT(128, 2) ATT(128, 4) ATT(128, 8)
     ATT(256, 1) ATT(256, 2) ATT(256, 4) ATT(256, 8)

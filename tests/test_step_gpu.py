@@ -467,10 +467,10 @@ def test_persistent_generate_one_launch_small(gpu, oracle):
 def test_graph_step_other_head_dims(gpu, oracle, head_dim, attn):
     """The hipGraph step at head_dim 64 and 256 (shapes with no persistent kernel: STEP_AUTO
     captures the graph), in both attention forms: QK-norm + RoPE inside the scores pass reading
-    the step's RoPE table (rope_table_kernel), and qk_norm_rope_forward + attention_forward.
-    Logits bit-identical to the oracle at positions 0-69 (crossing the first 64-position block)
-    of a prompt fed one token at a time, then a 24-token generate_greedy equal to the
-    oracle's."""
+    the step's RoPE table (rope_table_kernel), and qk_norm_rope_forward + attention_forward; at
+    these head dims the PV and combine passes are two launches. Logits bit-identical to the
+    oracle at positions 0-69 (crossing the first 64-position block) of a prompt fed one token at
+    a time, then a 24-token generate_greedy equal to the oracle's."""
     ident(f"graph step head_dim {head_dim} {attn}")
     from llm_inference_amd import model
     cfg = model.make_config(hidden_size=512, intermediate_size=1024, n_layers=2, n_heads=8,
@@ -497,6 +497,54 @@ def test_graph_step_other_head_dims(gpu, oracle, head_dim, attn):
             t = orc.forward(t, 70 + i, oracle.GPU_ORDER)
             want.append(t)
         assert got == want
+    finally:
+        dec.close()
+
+
+@pytest.mark.parametrize("n_heads", [4, 8, 16, 32])
+def test_graph_step_pv_combine_one_launch(gpu, oracle, n_heads):
+    """At head_dim 128 the graph step runs attention's PV and combine passes as one launch
+    (attn_pv_combine_kernel): every item publishes its block partials as tagged words and the
+    items of the T last blocks of each kv head add them in block order, T the largest power of
+    two <= min(blocks, REP * 128 / 16). 4 kv heads with n_heads / 4 = 1, 2, 4 or 8 query heads
+    each, a 16580-position N(0, 1) cache: logits bit-identical to the oracle at positions holding
+    1 to 260 blocks (T = 1 to 32; two staged chunks of partials past 256 blocks), in both
+    attention forms, then a short generate_greedy equal to the oracle's."""
+    ident(f"graph step one-launch PV + combine, {n_heads}/4 heads")
+    from llm_inference_amd import model
+    max_seq = 16640
+    cfg = model.make_config(hidden_size=512, intermediate_size=1024, n_layers=1,
+                            n_heads=n_heads, n_kv_heads=4, vocab_size=3000, max_seq_len=max_seq)
+    dec = model.Decoder(cfg, ("synth", 40 + n_heads, 0.02, 0.1))
+    try:
+        rng = np.random.default_rng(n_heads)
+        kvd = cfg.n_kv_heads * cfg.head_dim
+        k = np.zeros((1, max_seq, kvd), np.uint16)
+        v = np.zeros_like(k)
+        k[:, :16580] = rand_bf16(rng, (1, 16580, kvd))
+        v[:, :16580] = rand_bf16(rng, (1, 16580, kvd))
+        dec.set_kv_cache(k, v)
+        w = dec.host_weights()
+        orc = oracle.Model(oracle_cfg(cfg), w, max_seq=max_seq)
+        orc.bufs["key_cache"][:] = k.reshape(-1)
+        orc.bufs["value_cache"][:] = v.reshape(-1)
+        for attn in ("in_scores", "separate"):
+            dec.s.attn_mode = model.ATTN_MODES[attn]
+            dec.capture_graph("graph")
+            assert not dec.persistent
+            for pos in (0, 63, 64, 191, 500, 1023, 1100, 2100, 16383, 16384, 16579):
+                tok = int(rng.integers(0, cfg.vocab_size))
+                dec.forward(tok, pos)
+                nxt = dec.sample_argmax()
+                ref = orc.forward(tok, pos, oracle.GPU_ORDER)
+                assert np.array_equal(dec.logits(), orc.logits), (attn, pos)
+                assert nxt == ref, (attn, pos)
+            got = dec.generate_greedy(nxt, 16580, 6)
+            t, want = nxt, []
+            for i in range(6):
+                t = orc.forward(t, 16580 + i, oracle.GPU_ORDER)
+                want.append(t)
+            assert got == want, attn
     finally:
         dec.close()
 
