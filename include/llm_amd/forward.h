@@ -86,7 +86,9 @@ typedef struct {
     bf16 *k;
     bf16 *v;
     bf16 *attn_out;
-    float *att;            /* attention_workspace_floats(n_heads, head_dim, max_seq) */
+    float *att;            /* attention_workspace_floats(n_heads, head_dim, max_seq), then
+                              (from a 256-byte boundary) the launch counters and tagged block
+                              partials of the step's one-launch PV and combine (head_dim 128) */
     bf16 *key_cache;       /* [n_layers, max_seq, n_kv_heads * head_dim] */
     bf16 *value_cache;     /* [n_layers, max_seq, n_kv_heads * head_dim] */
     int max_seq;
@@ -136,9 +138,11 @@ typedef struct {
  * most 256 (64-position block, kv head) items, or when head_dim <= 128 and at most 4 query heads
  * share a kv head: every item then applies the query heads' QK-norm + RoPE with the step's RoPE
  * table (RunState::rope_table, one launch per step) and the scores kernel keeps five workgroups
- * per CU (Qwen3-0.6B graph step, 269 positions: +3% tokens/s; Qwen3-4B at 8448 positions: 420.6
- * tokens/s against 416.1 for ATTN_SEPARATE and 412.2 for ATTN_ONE_PASS). Otherwise
- * ATTN_SEPARATE. ATTN_ONE_PASS is taken only when asked for. */
+ * per CU (Qwen3-0.6B graph step, 269 positions: +3% tokens/s; Qwen3-4B at 8192-8448 positions:
+ * 433.3-433.8 tokens/s against 431.7 for ATTN_SEPARATE and 412.5 for ATTN_ONE_PASS). Otherwise
+ * ATTN_SEPARATE. ATTN_ONE_PASS is taken only when asked for. At head_dim 128 (and at most 8192
+ * items) the graph step's ATTN_IN_SCORES and ATTN_SEPARATE run attention's PV and combine passes
+ * as one launch, with the same bits. */
 enum { ATTN_AUTO = 0, ATTN_SEPARATE = 1, ATTN_IN_SCORES = 2, ATTN_ONE_PASS = 3 };
 
 /* How capture_graph prepares the step. STEP_AUTO: where the shapes have a specialisation
