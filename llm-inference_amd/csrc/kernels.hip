@@ -2005,6 +2005,14 @@ __global__ __launch_bounds__(256) void attn_pv_combine_kernel(PvCombineArgs o) {
     const uint32_t tag = (uint32_t)(launches % 0xffffffffull) + 1u;
     const int n = *a.d_pos + 1;
     const int nb = (n + ATT_B - 1) / ATT_B;
+    if (n <= 0 || n > a.max_seq) {  // every workgroup reads the same position: all skip
+        if (threadIdx.x == 0) {
+            __hip_atomic_store(gptr(o.err), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(gptr(ctr), launches + 1, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return;
+    }
     if ((int)blockIdx.x < nb * a.n_kv_heads) {  // the grid holds every item: one each
         const int b = blockIdx.x / a.n_kv_heads, g = blockIdx.x - b * a.n_kv_heads;
         pv_item<D, REP>(a, b, g, n, nb, p_s, red,
