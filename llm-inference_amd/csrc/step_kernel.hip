@@ -1205,7 +1205,8 @@ struct Shape {
     static constexpr int B_LM = H <= 2048 ? 4 : 2;  // 0.6B: 4 rows +0.4% over 8, 16 spills
     // copies of x, the attention output and the SwiGLU output (at most STEP_REPLICAS), each
     // 1 KB off the 4 KB grid (step_replica_stride): 4 at every shape (0.6B: 2291-2294 tokens/s
-    // against 2280-2282 with 8, on two boxes; 1.7B: 1115 against 1074)
+    // against 2280-2282 with 8, on two boxes, and 2301 against 2221 with 2 and 2067 with 3 on a
+    // third; 1.7B: 1115 against 1074 with 8)
     static constexpr int REPLICAS = 4;
     // 1.7B: the down rows with attention 1050 -> 1075 tokens/s, the q/k/v rows too 1005
     static constexpr int PF_D = H <= 2048 ? PF_WITH_ATTENTION : PF_AFTER_COMPUTE;
