@@ -549,6 +549,38 @@ def test_graph_step_pv_combine_one_launch(gpu, oracle, n_heads):
         dec.close()
 
 
+@pytest.mark.parametrize("n_heads,n_kv_heads,max_seq", [(8, 1, 100), (8, 8, 130), (2, 2, 64)])
+def test_graph_step_pv_combine_small_grids(gpu, oracle, n_heads, n_kv_heads, max_seq):
+    """The one-launch PV + combine on small grids: one kv head with 8 query heads (1024 columns,
+    4 per thread when one item combines them all), 8 kv heads of one query head, and a cache of
+    a single 64-position block (one item per kv head, which both computes and combines). Every
+    position of the cache stepped through in both attention forms: logits bit-identical to the
+    oracle."""
+    ident(f"graph step one-launch PV + combine, {n_heads}/{n_kv_heads} heads, {max_seq} slots")
+    from llm_inference_amd import model
+    cfg = model.make_config(hidden_size=512, intermediate_size=1024, n_layers=1,
+                            n_heads=n_heads, n_kv_heads=n_kv_heads, vocab_size=2000,
+                            max_seq_len=max_seq)
+    dec = model.Decoder(cfg, ("synth", 60 + n_heads + n_kv_heads, 0.02, 0.1))
+    try:
+        w = dec.host_weights()
+        orc = oracle.Model(oracle_cfg(cfg), w, max_seq=max_seq)
+        rng = np.random.default_rng(max_seq)
+        for attn in ("in_scores", "separate"):
+            dec.s.attn_mode = model.ATTN_MODES[attn]
+            dec.capture_graph("graph")
+            assert not dec.persistent
+            for pos in range(max_seq):
+                tok = int(rng.integers(0, cfg.vocab_size))
+                dec.forward(tok, pos)
+                nxt = dec.sample_argmax()
+                ref = orc.forward(tok, pos, oracle.GPU_ORDER)
+                assert np.array_equal(dec.logits(), orc.logits), (attn, pos)
+                assert nxt == ref, (attn, pos)
+    finally:
+        dec.close()
+
+
 def test_auto_step_switches_to_graph_at_switch_pos(gpu, oracle):
     """STEP_AUTO prepares the persistent kernel for the positions below its switch position
     (736 at hidden <= 1024) and the hipGraph from there on: single steps on either side of the
