@@ -1208,7 +1208,9 @@ struct Shape {
     // against 2280-2282 with 8, on two boxes, and 2301 against 2221 with 2 and 2067 with 3 on a
     // third; 1.7B: 1115 against 1074 with 8)
     static constexpr int REPLICAS = 4;
-    // 1.7B: the down rows with attention 1050 -> 1075 tokens/s, the q/k/v rows too 1005
+    // 1.7B: the down rows with attention 1050 -> 1075 tokens/s, the q/k/v rows too 1005; 4B
+    // (5-token prompt): 575.8-576.4 as below, the q/k/v rows after the gate/up poll 572.6-572.8,
+    // the down rows after the o poll 466.2-466.3
     static constexpr int PF_D = H <= 2048 ? PF_WITH_ATTENTION : PF_AFTER_COMPUTE;
     static constexpr int PF_QKV = H <= 1024 ? PF_WITH_ATTENTION : PF_AFTER_COMPUTE;
     // separate token loops for the two roles: 0.6B +1.7%; 1.7B -1.8% (its one shared loop
