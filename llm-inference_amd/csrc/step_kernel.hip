@@ -1198,11 +1198,12 @@ struct Shape {
     // kernel 424 + 0.53 us per position at 0.6B, 892 + 0.52 at 1.7B, 1730 + 0.72 at 4B; hipGraph
     // 783 + 0.024, 1120 + 0.016, 2032 + 0.02 (us per token)
     static constexpr int SWITCH_POS = H <= 1024 ? 736 : H <= 2048 ? 480 : 448;
-    static constexpr int B_QKV = H <= 1024 ? 4 : 2;
+    static constexpr int B_QKV = H <= 1024 ? 4 : 2;  // 4B: 575.4-575.9 tokens/s, 1 row 544.7
     static constexpr int B_O = H <= 1024 ? 1 : (HQ * 128 <= 2048 ? 2 : 1);
     static constexpr int B_GU = H <= 1024 ? 2 : 1;
     static constexpr int B_DOWN = 1;
-    static constexpr int B_LM = H <= 2048 ? 4 : 2;  // 0.6B: 4 rows +0.4% over 8, 16 spills
+    // 0.6B: 4 rows +0.4% over 8, 16 spills; 4B: 4 rows spill (156 bytes), 561.1 against 575.4
+    static constexpr int B_LM = H <= 2048 ? 4 : 2;
     // copies of x, the attention output and the SwiGLU output (at most STEP_REPLICAS), each
     // 1 KB off the 4 KB grid (step_replica_stride): 4 at every shape (0.6B: 2291-2294 tokens/s
     // against 2280-2282 with 8, on two boxes, and 2301 against 2221 with 2 and 2067 with 3 on a
