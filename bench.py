@@ -3,24 +3,24 @@
 Workload (the headline metric's tokens/s half): Qwen3-0.6B shapes (28 layers, hidden 1024, 16q/8kv
 heads of 128, intermediate 3072, vocab 151936, tied embeddings), seeded random weights N(0, 0.02)
 and norm gammas 1 + N(0, 0.1), batch 1, a 5-token prompt of seeded uniform ids, then greedy decode.
-A step is one decode token. The protocol is the reference's (src/main.cu:110-148): one warm-up run
-(--warmup tokens), then 5 runs of exactly --steps tokens, each bracketed by device syncs and
-generated by the captured step replayed on the device (argmax fed back, no host round trip per
-token); `value` is --steps / the median run time.
+A step is the metric's Qwen3-0.6B workload: 256 greedy tokens after the 5-token prompt (positions
+5-260), decoded by one generate call on the device (argmax fed back, no host round trip per
+token), as in the reference's protocol (src/main.cu:110-148). --warmup steps run untimed, then
+exactly --steps steps in one timed region bracketed by device syncs; `value` is the generated
+tokens / the region's seconds, `ms_per_step` the region's milliseconds per step.
 
 The JSON line also carries:
   device_peak   the device's copy and read bandwidth as the reference measures them beside every
-                run (bench/bandwidth.cu: a 512 MiB device-to-device copy, median of 20 after 200
-                warm-ups; a 512 MiB read, median of 20, best of 15 launch shapes)
-  roofline      the dominant kernel: the persistent step kernel (ONE launch decodes every timed
-                token: all layers, the LM head and the argmax, the argmax fed to the next token
-                inside the kernel), timed with HIP events on the step's stream (median of the 5
-                runs), as algorithmic bytes per launch (per token: all weights + the KV history
-                read at that position) / launch time vs 8 TB/s and vs the measured read peak;
+                run (bench/bandwidth.cu: a 1 GiB device-to-device copy, median of 20 after 200
+                warm-ups; a 1 GiB read, median of 20, best of 45 launch shapes)
+  roofline      the dominant kernel: the persistent step kernel (ONE launch decodes a step's 256
+                tokens: all layers, the LM head and the argmax, the argmax fed to the next token
+                inside the kernel), timed with HIP events on the step's stream (mean over the
+                timed steps), as algorithmic bytes per launch (per token: all weights + the KV
+                history read at that position) / launch time vs 8 TB/s and vs the read peak;
                 traffic (HBM bytes per launch) from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
                 summary of the same launch
-  qwen3_0.6B_256  the metric's Qwen3-0.6B config exactly (5-token prompt, 256 tokens, median of
-                5), whatever --steps is
+  qwen3_0.6B_256  the same steps as the reference reports them: the median step's tokens/s
   fused_kernels the fused-kernel GB/s at Qwen3-4B widths, the many-row sweep sizes and the
                 Qwen3-0.6B layer's decode kernels (config 1), each timed
                 over rotating buffers larger than the 256 MB MALL, against 8 TB/s and against
@@ -43,7 +43,8 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parent
 PKG_DIR = ROOT / "llm-inference_amd"
 HBM_PEAK_GBS = 8000.0
-RUNS = 5  # timed runs per measurement; the median is reported (src/main.cu:110-148)
+RUNS = 5  # timed runs per decode config; the median is reported (src/main.cu:110-148)
+GEN_TOKENS = 256  # greedy tokens of one bench step (the metric's Qwen3-0.6B config)
 METRIC = "fused-kernel HBM GB/s (% of 8 TB/s); decode tokens/s Qwen3-0.6B/4B bs=1"
 
 
@@ -89,11 +90,11 @@ def rotating(n_bytes_each, min_total=512 << 20, max_copies=64):
 
 def device_peak(pkg, stream):
     """The device's copy and read bandwidth, measured as bench/bandwidth.cu:25-116 does: a
-    512 MiB device-to-device copy (median of 20 after 200 warm-ups; a copy moves 2x the bytes),
-    then a 512 MiB read (hbm_read_peak_probe), median of 20 after 3 warm-ups per launch shape,
-    the best of 3 workgroup sizes x 5 workgroups-per-CU counts."""
+    1 GiB device-to-device copy (median of 20 after 200 warm-ups; a copy moves 2x the bytes),
+    then a 1 GiB read (hbm_read_peak_probe), median of 20 after 3 warm-ups per launch shape,
+    the best of 3 workgroup sizes x 5 workgroups-per-CU counts x 3 loads-in-flight counts."""
     import torch
-    nbytes = 512 << 20
+    nbytes = 1 << 30
     L = pkg.lib()
     src = torch.empty(nbytes // 2, dtype=torch.int16, device="cuda")
     L.synth_fill(src.data_ptr(), src.numel(), 321, 0, 0.0, 1.0, stream)
@@ -118,19 +119,21 @@ def device_peak(pkg, stream):
     copy_gbs = 2 * nbytes / (copy_ms * 1e-3) / 1e9
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     shapes = {}
-    for threads in (256, 512, 1024):
-        for per_cu in (1, 2, 4, 8, 16):
-            blocks = per_cu * cus
-            ms = median_ms(lambda: pkg.hbm_read_peak_probe(out, src, nbytes, blocks, threads,
-                                                           stream=stream), 3, 20)
-            shapes[f"{blocks}x{threads}"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+    for loads in (4, 8, 16):
+        for threads in (256, 512, 1024):
+            for per_cu in (1, 2, 4, 8, 16):
+                blocks = per_cu * cus
+                ms = median_ms(lambda: pkg.hbm_read_peak_probe(out, src, nbytes, blocks, threads,
+                                                               loads, stream=stream), 3, 20)
+                shapes[f"{blocks}x{threads}x{loads}"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
     best = max(shapes, key=shapes.get)
     torch.cuda.synchronize()
     del src, dst
     res = {"copy_GB/s": round(copy_gbs, 1), "read_GB/s": shapes[best], "read_best_shape": best,
            "read_shapes_GB/s": shapes, "bytes": nbytes,
-           "method": "bench/bandwidth.cu: 512 MiB D2D copy (2x bytes), median of 20 after 200 "
-                     "warm-ups; 512 MiB read, median of 20, best of 15 launch shapes"}
+           "method": "bench/bandwidth.cu: 1 GiB D2D copy (2x bytes), median of 20 after 200 "
+                     "warm-ups; 1 GiB read, median of 20, best of 45 launch shapes "
+                     "(workgroups x threads x 16-byte loads in flight per thread)"}
     log(f"device peak: copy {res['copy_GB/s']} GB/s, read {res['read_GB/s']} GB/s ({best})")
     return res
 
@@ -712,8 +715,9 @@ def decode_config(size, n_prefill, steps, cpu_budget_s, read_peak=None):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=256)
-    ap.add_argument("--warmup", type=int, default=32)
+    ap.add_argument("--steps", type=int, default=10,
+                    help="timed steps; a step is 256 greedy Qwen3-0.6B tokens after the prompt")
+    ap.add_argument("--warmup", type=int, default=2, help="untimed steps before them")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-kernel-table", action="store_true")
     ap.add_argument("--no-device-peak", action="store_true")
@@ -743,7 +747,7 @@ def main():
         sys.exit(2)
 
     if args.pmc_workload:
-        pmc_workload(args.steps)
+        pmc_workload(GEN_TOKENS)
     elif args.gemv_workload:
         gemv_workload()
     elif args.config4_workload:
@@ -764,8 +768,8 @@ def run_bench(args):
     from llm_inference_amd import model
     assert torch.cuda.is_available(), "bench.py needs the GPU"
     pkg.lib()
-    n_prompt = 5
-    max_seq = n_prompt + max(args.steps, args.warmup, 256) + 8
+    n_prompt, n_gen = 5, GEN_TOKENS
+    max_seq = n_prompt + n_gen + 8
     cfg = model.qwen3_config("0.6B", max_seq_len=max_seq)
     log(f"building Qwen3-0.6B synthetic weights (seed 0), KV cache {max_seq} positions")
     dec = model.Decoder(cfg, ("synth", 0, 0.02, 0.1))
@@ -776,64 +780,73 @@ def run_bench(args):
     for pos, tok in enumerate(prompt):
         dec.forward(tok, pos)
     first = dec.sample_argmax()
-    # the workload of src/main.cu:110-148: the prompt, then a warm-up run and RUNS timed runs of
-    # `steps` greedy tokens from the same position
-    dt, ev_dt, walls, tokens = timed_runs(dec, first, n_prompt, args.steps, args.warmup)
-    tok_s = args.steps / dt
-    # the persistent path decodes a run's tokens in one launch; the hipGraph step is one replay
-    # per token (STEP_AUTO switches from the one to the other at step_switch_pos)
-    k_tok = dec.kernel_tokens(n_prompt, args.steps)
-    all_kernel = k_tok == args.steps
-    launches = (1 if k_tok else 0) + args.steps - k_tok
-    per_launch = ev_dt / launches  # seconds per launch by HIP events (median run)
-    log(f"decode: {args.steps} tokens, median of {RUNS} runs {dt * 1e3:.2f} ms -> "
-        f"{tok_s:.1f} tokens/s ({dec.step_kind(n_prompt, args.steps)}, "
-        f"{launches} launch(es) of {per_launch * 1e6:.1f} us by HIP events); runs "
-        + ", ".join(f"{args.steps / w:.1f}" for w in walls))
+    # A step is the metric's Qwen3-0.6B workload: 256 greedy tokens from position 5, after the
+    # 5-token prompt, decoded by one generate call (src/main.cu:110-148). --warmup steps run
+    # untimed, then exactly --steps steps inside one timed region bracketed by device syncs;
+    # HIP events on the step's stream time each step's device work.
+    k_tok = dec.kernel_tokens(n_prompt, n_gen)
+    launches = (1 if k_tok else 0) + n_gen - k_tok  # per step
+    for _ in range(args.warmup):
+        dec.generate_greedy(first, n_prompt, n_gen)
+    stream = torch.cuda.ExternalStream(dec.stream)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    walls, tokens = [], None
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        t_i = time.perf_counter()
+        evs[i][0].record(stream)
+        got = dec.generate_greedy(first, n_prompt, n_gen)  # ends with a host sync (its tokens)
+        evs[i][1].record(stream)
+        walls.append(time.perf_counter() - t_i)
+        if tokens is not None and got != tokens:
+            raise RuntimeError("bench: two runs of the same greedy decode differ")
+        tokens = got
+    torch.cuda.synchronize()
+    total = time.perf_counter() - t0
+    ev_s = [a.elapsed_time(b) / 1e3 for a, b in evs]
+    tok_s = n_gen * args.steps / total
+    per_launch = statistics.mean(ev_s) / launches  # seconds per launch by HIP events
+    log(f"decode: {args.steps} steps of {n_gen} tokens in {total * 1e3:.1f} ms -> "
+        f"{tok_s:.1f} tokens/s ({dec.step_kind(n_prompt, n_gen)}, {launches} launch(es) per "
+        f"step of {per_launch * 1e6:.1f} us by HIP events); steps "
+        + ", ".join(f"{n_gen / w:.1f}" for w in walls))
 
     wbytes = dec.weight_bytes_per_step()
     kvb = dec.kv_bytes_per_position()
-
-    def step_bytes_at(steps):  # bench/bench.py:139-142: step i attends n_prompt + i + 1 positions
-        return wbytes + kvb * (n_prompt + (steps + 1) / 2)
-
-    step_bytes = step_bytes_at(args.steps)
-    eff_gbs = step_bytes / (dt / args.steps) / 1e9
-
-    # the metric's config exactly: 5-token prompt, 256 tokens, median of RUNS
-    if args.steps == 256:
-        c256 = (dt, walls)
-    else:
-        d256, _, w256, _ = timed_runs(dec, first, n_prompt, 256, args.warmup)
-        c256 = (d256, w256)
-    b256 = step_bytes_at(256)
+    # bench/bench.py:139-142: generated token i attends n_prompt + i + 1 positions
+    tok_bytes = wbytes + kvb * (n_prompt + (n_gen + 1) / 2)
+    eff_gbs = tok_bytes * tok_s / 1e9
+    med = statistics.median(walls)
     qwen3_06b_256 = {
-        "tokens_per_s": round(256 / c256[0], 2), "ms_per_token": round(c256[0] * 1e3 / 256, 4),
-        "steps": 256, "start_position": n_prompt, "runs": RUNS,
-        "run_tokens_per_s": [round(256 / w, 2) for w in c256[1]],
-        "bytes_per_token": int(b256),
-        "effective_GB/s": round(b256 * 256 / c256[0] / 1e9, 1),
-        "frac_of_8TBs": round(b256 * 256 / c256[0] / 1e9 / HBM_PEAK_GBS, 4),
-        "frac_of_read_peak": round(b256 * 256 / c256[0] / 1e9 / read_peak, 4) if read_peak else None}
-    log(f"Qwen3-0.6B, 5 + 256 tokens: {qwen3_06b_256['tokens_per_s']} tokens/s "
-        f"({qwen3_06b_256['frac_of_8TBs']:.1%} of 8 TB/s)")
+        "tokens_per_s": round(n_gen / med, 2), "ms_per_token": round(med * 1e3 / n_gen, 4),
+        "steps": n_gen, "start_position": n_prompt, "runs": len(walls),
+        "protocol": "median of the timed steps (src/main.cu:110-148)",
+        "bytes_per_token": int(tok_bytes),
+        "effective_GB/s": round(tok_bytes * n_gen / med / 1e9, 1),
+        "frac_of_8TBs": round(tok_bytes * n_gen / med / 1e9 / HBM_PEAK_GBS, 4),
+        "frac_of_read_peak": (round(tok_bytes * n_gen / med / 1e9 / read_peak, 4)
+                              if read_peak else None)}
+    log(f"Qwen3-0.6B, 5 + 256 tokens: {tok_s:.2f} tokens/s over the timed region, median step "
+        f"{qwen3_06b_256['tokens_per_s']} ({eff_gbs / HBM_PEAK_GBS:.1%} of 8 TB/s)")
 
     # the reference's per-token protocol: host-visible token every step (forward + sample_argmax)
     t0 = time.perf_counter()
     t = first
-    for i in range(min(args.steps, 64)):
+    for i in range(64):
         dec.forward(t, n_prompt + i)
         t = dec.sample_argmax()
-    hs_dt = (time.perf_counter() - t0) / min(args.steps, 64)
+    hs_dt = (time.perf_counter() - t0) / 64
     log(f"host-synced loop: {1 / hs_dt:.1f} tokens/s")
 
     # dominant kernel: the step kernel over the timed region
     c = dec.cfg
     I, H = c.intermediate_size, c.hidden_size
-    launch_bytes = step_bytes * args.steps / launches
+    launch_bytes = tok_bytes * n_gen / launches
     achieved = launch_bytes / per_launch / 1e9
     log(f"step kernel: {launch_bytes / 1e6:.1f} MB per launch, {achieved:.1f} GB/s")
-    traffic = traffic_from_profiles(args.steps // launches) if all_kernel else None
+    traffic = traffic_from_profiles(n_gen) if launches == 1 else None
 
     table = None if args.no_kernel_table else fused_kernel_table(pkg, dec.stream, read_peak)
     if table and not args.no_cpu_baseline:
@@ -849,34 +862,34 @@ def run_bench(args):
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(dt * 1e3 / args.steps, 4),
+        "ms_per_step": round(total * 1e3 / args.steps, 3),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded N(0,0.02) weights, gammas 1+N(0,0.1), uniform prompt ids)",
-        "config": {"workload": "Qwen3-0.6B greedy decode, batch 1, 5-token prompt then "
-                               f"{args.steps} tokens, on-device token feedback",
+        "config": {"workload": "Qwen3-0.6B greedy decode, batch 1: a step is 256 greedy tokens "
+                               "after the 5-token prompt (positions 5-260), on-device token "
+                               "feedback; value = generated tokens / timed seconds",
                    "layers": c.n_layers, "hidden": H, "heads": [c.n_heads, c.n_kv_heads],
                    "head_dim": c.head_dim, "intermediate": I, "vocab": c.vocab_size,
-                   "global_batch": 1, "seq_len": n_prompt + args.steps,
-                   "parallelism": "single GPU"},
+                   "global_batch": 1, "seq_len": n_prompt + n_gen,
+                   "tokens_per_step": n_gen, "parallelism": "single GPU"},
         "roofline": {"bound": "hbm",
-                     "kernel": f"step_kernel (persistent: one launch decodes {args.steps} "
-                               "tokens, each 28 layers + LM head + argmax)" if all_kernel
-                               else dec.step_kind(n_prompt, args.steps) + " (mean per launch)",
+                     "kernel": f"step_kernel (persistent: one launch decodes the step's {n_gen} "
+                               "tokens, each 28 layers + LM head + argmax)" if launches == 1
+                               else dec.step_kind(n_prompt, n_gen) + " (mean per launch)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "frac_of_read_peak": round(achieved / read_peak, 4) if read_peak else None,
                      "bytes_per_launch": int(launch_bytes),
                      "us_per_launch": round(per_launch * 1e6, 3),
-                     "us_per_token": round(per_launch * launches / args.steps * 1e6, 3)},
-        "decode_roofline": {"bytes_per_token": int(step_bytes),
+                     "us_per_token": round(per_launch * launches / n_gen * 1e6, 3)},
+        "decode_roofline": {"bytes_per_token": int(tok_bytes),
                             "effective_GB/s": round(eff_gbs, 1),
                             "frac_of_8TBs": round(eff_gbs / HBM_PEAK_GBS, 4),
                             "frac_of_read_peak": round(eff_gbs / read_peak, 4) if read_peak else None},
-        "runs": RUNS,
-        "run_tokens_per_s": [round(args.steps / w, 2) for w in walls],
+        "step_tokens_per_s": [round(n_gen / w, 2) for w in walls],
         "qwen3_0.6B_256": qwen3_06b_256,
         "device_peak": peak,
         "host_sync": {"tokens_per_s": round(1 / hs_dt, 2),
@@ -889,8 +902,8 @@ def run_bench(args):
     }
     dec.close()
     if not args.no_configs:
-        # the other decode configs of the metric: Qwen3-1.7B after a 5-token prompt, and
-        # Qwen3-4B after an 8192-position cache (mean position 8320.5), 256 tokens each
+        # the other decode configs of the metric: Qwen3-1.7B and Qwen3-4B after a 5-token prompt,
+        # and Qwen3-4B after an 8192-position cache (mean position 8320.5), 256 tokens each
         budget = 0 if args.no_cpu_baseline else 10.0
         line["decode_configs"] = {
             "qwen3_1.7B": decode_config("1.7B", 0, 256, budget, read_peak),

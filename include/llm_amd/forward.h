@@ -146,7 +146,7 @@ typedef struct {
 enum { ATTN_AUTO = 0, ATTN_SEPARATE = 1, ATTN_IN_SCORES = 2, ATTN_ONE_PASS = 3 };
 
 /* How capture_graph prepares the step. STEP_AUTO: where the shapes have a specialisation
- * (Qwen3-0.6B, 1.7B, 4B), the persistent step kernel (one cooperative launch per forward;
+ * (Qwen3-0.6B, 1.7B, 4B), the persistent step kernel (one launch per forward;
  * generate_greedy runs its tokens in one launch) for the positions below
  * RunState::step_switch_pos, and a hipGraph of the per-layer kernels from there on: the kernel's
  * attention runs one workgroup per query head, so its cost grows with the history faster than

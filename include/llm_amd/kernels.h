@@ -61,10 +61,15 @@ void qk_norm_rope_forward(bf16 *q, bf16 *k, const bf16 *v, const bf16 *q_norm_w,
 
 /* src/kernels.cuh:22-24. Decode attention of the query at position *d_pos over cache rows
  * 0..*d_pos, GQA kv_head = h / (n_heads / n_kv_heads). scores bf16(bf16(q.k) * scale), softmax
- * probabilities rounded to bf16, out = bf16(sum p v). `att` is 16-byte aligned fp32 scratch of
- * at least attention_workspace_floats(n_heads, head_dim, max_seq) floats: the reference's
- * [n_heads, max_seq] score rows followed by the split-softmax block statistics and partial
- * outputs. head_dim in {64, 128, 256}; n_heads / n_kv_heads in {1, 2, 4, 8}. */
+ * probabilities rounded to bf16, out = bf16(sum p v). `att` is 16-byte aligned fp32 scratch
+ * holding either the reference's [n_heads, max_seq] score rows (src/forward.cuh:13) or
+ * attention_workspace_floats(n_heads, head_dim, max_seq) floats: the score rows followed by the
+ * split softmax's block statistics and partial outputs. With the reference's size, those live
+ * in a library-owned device array of 2^22 floats per device (n_heads * ceil(max_seq / 64) *
+ * (head_dim + 2) floats must fit; larger sizes are an error), and calls on one device that use
+ * it must not overlap. A smaller `att` is an error. The size is what the runtime reports for the
+ * allocation holding `att`, counted from `att` to its end. head_dim in {64, 128, 256};
+ * n_heads / n_kv_heads in {1, 2, 4, 8}. */
 void attention_forward(bf16 *out, const bf16 *q, const bf16 *key_cache, const bf16 *value_cache,
                        float *att, int n_heads, int n_kv_heads, int head_dim, const int *d_pos,
                        int max_seq, float scale, hipStream_t stream);
@@ -154,16 +159,18 @@ void hbm_stream_probe(void *dst, const void *a, const void *b, size_t n_bytes, i
                       hipStream_t stream);
 
 /* Measurement helper: the device read peak, as the reference measures it beside every bench run
- * (bench/bandwidth.cu:25-116 read_kernel: a grid-stride read over 512 MiB, the best of several
- * launch shapes). Reads n_bytes of a (n_bytes % 16 == 0, 16-byte aligned) with `blocks`
- * workgroups of `threads` threads (64..1024, a power of two); *out is written only in the
- * unlikely case the xor of a thread's data equals 0x9e3779b9. */
+ * (bench/bandwidth.cu:25-116 read_kernel: a grid-stride read, the best of several launch
+ * shapes). Reads n_bytes of a (n_bytes % 16 == 0, 16-byte aligned) with `blocks` workgroups of
+ * `threads` threads (64..1024, a power of two), each thread keeping loads_in_flight (4, 8 or 16)
+ * non-temporal 16-byte loads in flight per round; *out is written only in the unlikely case the
+ * xor of a thread's data equals 0x9e3779b9. */
 void hbm_read_peak_probe(unsigned *out, const void *a, size_t n_bytes, int blocks, int threads,
-                         hipStream_t stream);
+                         int loads_in_flight, hipStream_t stream);
 
-/* No counterpart in the reference: attention_forward (src/kernels.cuh:22-24) without the `att`
- * argument, for callers that cannot allocate device memory (code under stream capture, tight
- * serving loops, harnesses that forbid hipMalloc). It allocates nothing: its workspace is a
+/* No counterpart in the reference. Decode attention as attention_forward computes it, without
+ * the `att` argument, for callers that cannot allocate device memory (code under stream
+ * capture, tight serving loops, harnesses that forbid hipMalloc). It allocates nothing: its
+ * workspace is a
  * library-owned device array of 2^20 floats (4 MiB) per device, so
  * attention_workspace_floats(n_heads, head_dim, max_seq) must not exceed 1048576 (Qwen3-4B's 32
  * heads of 128 fit up to 10798 positions); larger sizes are an error and nothing is launched.

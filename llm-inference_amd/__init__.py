@@ -74,7 +74,7 @@ _SIGS = {
     "rmsnorm_gemv_forward": (None, [_vp] * 4 + [_f, _i, _i, _vp]),
     "rmsnorm_gate_up_forward": (None, [_vp] * 5 + [_f, _i, _i, _vp]),
     "hbm_stream_probe": (None, [_vp, _vp, _vp, _sz, _i, _vp]),
-    "hbm_read_peak_probe": (None, [_vp, _vp, _sz, _i, _i, _vp]),
+    "hbm_read_peak_probe": (None, [_vp, _vp, _sz, _i, _i, _i, _vp]),
     "qk_norm_rope_attention_forward": (None, [_vp] * 9 + [_vp, _i, _i, _i, _f, _f, _i, _f, _vp]),
     "qk_norm_rope_attention_one_pass": (None, [_vp] * 11 + [_i, _i, _i, _f, _f, _i, _f, _vp]),
     "attention_one_pass_bytes": (_sz, [_i, _i, _i]),
@@ -231,6 +231,10 @@ def attention_workspace_floats(n_heads, head_dim, max_seq):
 
 def attention_forward(out, q, key_cache, value_cache, att, n_heads, n_kv_heads, head_dim, d_pos,
                       max_seq, scale, stream=None):
+    """att: a device pointer (int) to the caller's own allocation of at least [n_heads, max_seq]
+    floats (the library checks that allocation's size), or a torch tensor of at least
+    attention_workspace_floats(n_heads, head_dim, max_seq) floats: torch's caching allocator
+    carves tensors out of larger allocations, whose size says nothing of the tensor's."""
     need = attention_workspace_floats(n_heads, head_dim, max_seq)
     if not isinstance(att, int) and att.numel() < need:
         raise LlmError(f"att holds {att.numel()} floats, attention needs {need}")
@@ -291,11 +295,12 @@ def hbm_stream_probe(dst, a, b, n_bytes, mode, stream=None):
     _call(lib().hbm_stream_probe, _ptr(dst), _ptr(a), _ptr(b), n_bytes, mode, _stream(stream))
 
 
-def hbm_read_peak_probe(out, a, n_bytes, blocks, threads, stream=None):
-    """Reads n_bytes of `a` with `blocks` workgroups of `threads` threads (the read-peak probe);
-    `out` is a device word written only if a thread's xor equals 0x9e3779b9."""
+def hbm_read_peak_probe(out, a, n_bytes, blocks, threads, loads_in_flight=4, stream=None):
+    """Reads n_bytes of `a` with `blocks` workgroups of `threads` threads, loads_in_flight
+    16-byte loads per thread per round (the read-peak probe); `out` is a device word written
+    only if a thread's xor equals 0x9e3779b9."""
     _call(lib().hbm_read_peak_probe, _ptr(out), _ptr(a), n_bytes, blocks, threads,
-          _stream(stream))
+          loads_in_flight, _stream(stream))
 
 
 def sample_forward(out, x, n, inv_temp, u, stream=None):

@@ -204,6 +204,27 @@ __device__ __forceinline__ void scatter_keep(const float *v, float *out) {
     }
 }
 
+// Error flag of the bounded waits between workgroups: 0 none, 1 a token or position out of
+// range, 2 a wait that ran out of polls. A wait that sees the flag set stops at once and leaves
+// the code as it is; a wait that runs out sets 2 only if no earlier error set the flag.
+__device__ __forceinline__ bool wait_error_set(const int *err) {
+    return __hip_atomic_load(gptr((int *)err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0;
+}
+__device__ __forceinline__ void wait_timed_out(int *err) {
+    int expected = 0;
+    __hip_atomic_compare_exchange_strong(gptr(err), &expected, 2, __ATOMIC_RELAXED,
+                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// One check of a bounded wait, every few polls: true once the wait must stop.
+__device__ __forceinline__ bool wait_gives_up(long long spins, long long limit, int *err) {
+    if (wait_error_set(err)) return true;
+    if (spins > limit) {
+        wait_timed_out(err);
+        return true;
+    }
+    return false;
+}
+
 // Larger value wins, equal values keep the lower index; NaN is never taken.
 __device__ __forceinline__ void amax_pair(float &v, int &i, float v2, int i2) {
     if (v2 > v || (v2 == v && i2 < i)) {

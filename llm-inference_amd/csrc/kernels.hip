@@ -1479,8 +1479,8 @@ __device__ __forceinline__ void op_st(unsigned long long *p, float v, uint32_t t
 
 // Polls the tagged words addr(idx), idx = threadIdx.x + NT k < total (NT threads in the
 // workgroup, K words of a thread in flight), until every tag is `tag`, and hands each value to
-// put(idx, value). Bounded: on timeout, or once another workgroup has timed out, it sets *err and
-// goes on with what it read.
+// put(idx, value). Bounded: once *err is set (by another wait or an earlier error), or when its
+// own polls run out (then *err = 2 unless already set), it goes on with what it read.
 template <int NT = OP_THREADS, int K = 8, class Addr, class Put>
 __device__ __forceinline__ void op_poll(int total, uint32_t tag, int *err, Addr addr, Put put) {
     for (int base = 0; base < total; base += NT * K) {
@@ -1495,12 +1495,7 @@ __device__ __forceinline__ void op_poll(int total, uint32_t tag, int *err, Addr 
                 fresh &= idx >= total || (uint32_t)wv[k] == tag;
             }
             if (fresh) break;
-            if ((++spins & 15) == 0 &&
-                (spins > OP_SPIN_LIMIT ||
-                 __hip_atomic_load(gptr(err), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
-                __hip_atomic_store(gptr(err), 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
+            if ((++spins & 15) == 0 && wait_gives_up(spins, OP_SPIN_LIMIT, err)) break;
         }
 #pragma unroll
         for (int k = 0; k < K; k++) {
@@ -2114,23 +2109,68 @@ static void launch_attention_t(const AttnArgs &a, int grid, hipStream_t stream,
     LAUNCH_OK();
 }
 
-// The caller's `att` must hold attention_workspace_floats() floats, more than the reference's
-// [n_heads, max_seq] scores: a caller that sized it the reference's way gets an error, not an
-// overrun, wherever the runtime knows the allocation holding `att` (a buffer carved out of a
-// larger allocation passes if that allocation is large enough).
-static bool check_att_size(const float *att, int n_heads, int head_dim, int max_seq) {
+// Block statistics and partial outputs of attention_forward for a caller whose `att` holds only
+// the reference's [n_heads, max_seq] scores (src/forward.cu:10-51 sizes it so): a library-owned
+// device array of 2^22 floats (16 MiB) per device, as argmax_forward keeps its partials. Every
+// value a call reads from it was written earlier in the same call, so nothing is cleared; calls
+// on one device that use it must not overlap.
+constexpr size_t ATTN_BLOCK_FLOATS = (size_t)1 << 22;
+static __device__ __align__(256) float g_attn_blocks[ATTN_BLOCK_FLOATS];
+
+static float *attn_blocks_on_current_device() {
+    static std::mutex mu;
+    static float *addr[64];
+    int dev = 0;
+    if (!HIP_OK(hipGetDevice(&dev))) return nullptr;
+    if (dev < 0 || dev >= 64) {
+        llm_fail("attention: device %d out of range", dev);
+        return nullptr;
+    }
+    std::lock_guard<std::mutex> lock(mu);
+    if (!addr[dev]) {
+        float *p = nullptr;
+        if (!HIP_OK(hipGetSymbolAddress((void **)&p, HIP_SYMBOL(g_attn_blocks)))) return nullptr;
+        addr[dev] = p;
+    }
+    return addr[dev];
+}
+
+// Where the split softmax keeps its block statistics and partial outputs. An `att` with room for
+// attention_workspace_floats() floats holds them after the scores. An `att` sized the
+// reference's way, [n_heads, max_seq] floats, holds the scores only, and the rest goes to the
+// library's array. A smaller `att` is an error, not an overrun. The room is what the runtime
+// knows of the allocation holding `att` (a buffer carved out of a larger allocation counts to
+// that allocation's end); where it knows nothing, `att` is taken to hold the whole workspace.
+static bool attention_blocks(float *att, int n_heads, int head_dim, int max_seq, float **stats,
+                             float **partial) {
+    *stats = att + (size_t)n_heads * max_seq;
+    *partial = att + attention_partial_offset(n_heads, max_seq);
     hipDeviceptr_t base = nullptr;
     size_t bytes = 0;
     if (hipMemGetAddressRange(&base, &bytes, (hipDeviceptr_t)att) != hipSuccess || !base) {
         (void)hipGetLastError();  // not a runtime allocation: nothing to check against
         return true;
     }
-    const size_t need = attention_workspace_floats(n_heads, head_dim, max_seq) * sizeof(float);
     const size_t avail = bytes - (size_t)((const char *)att - (const char *)base);
-    if (avail < need)
-        return llm_fail("attention: att has room for %zu bytes, the workspace needs %zu "
-                        "(attention_workspace_floats(%d, %d, %d) floats)",
-                        avail, need, n_heads, head_dim, max_seq);
+    const size_t need = attention_workspace_floats(n_heads, head_dim, max_seq) * sizeof(float);
+    if (avail >= need) return true;
+    const size_t scores = (size_t)n_heads * max_seq * sizeof(float);
+    if (avail < scores)
+        return llm_fail("attention: att has room for %zu bytes, fewer than the %zu of its "
+                        "[%d, %d] scores", avail, scores, n_heads, max_seq);
+    const size_t mb = ceil_div((size_t)max_seq, ATT_B);
+    const size_t stat_floats = ceil_div((size_t)n_heads * mb * 2, 4) * 4;
+    const size_t block_floats = stat_floats + (size_t)n_heads * mb * head_dim;
+    if (block_floats > ATTN_BLOCK_FLOATS)
+        return llm_fail("attention: att holds the [%d, %d] scores only, and the %zu floats of "
+                        "block statistics and partials exceed the library's %zu (give att "
+                        "attention_workspace_floats(%d, %d, %d) floats)",
+                        n_heads, max_seq, block_floats, ATTN_BLOCK_FLOATS, n_heads, head_dim,
+                        max_seq);
+    float *blocks = attn_blocks_on_current_device();
+    if (!blocks) return false;
+    *stats = blocks;
+    *partial = blocks + stat_floats;
     return true;
 }
 
@@ -2149,15 +2189,16 @@ static bool attention_args(AttnArgs &a, int &grid, bf16 *out, const bf16 *q,
     if (max_seq <= 0) return llm_fail("attention: max_seq %d must be positive", max_seq);
     if (!aligned16(q) || !aligned16(key_cache) || !aligned16(value_cache) || !aligned16(att))
         return llm_fail("attention: q, the caches and att must be 16-byte aligned");
-    if (att && !check_att_size(att, n_heads, head_dim, max_seq)) return false;
+    float *stats = nullptr, *partial = nullptr;
+    if (!attention_blocks(att, n_heads, head_dim, max_seq, &stats, &partial)) return false;
     a.out = out;
     a.q = q;
     a.kc = key_cache;
     a.vc = value_cache;
     a.max_blocks = (int)ceil_div((size_t)max_seq, ATT_B);
     a.scores = att;
-    a.stats = att + (size_t)n_heads * max_seq;
-    a.partial = att + attention_partial_offset(n_heads, max_seq);
+    a.stats = stats;
+    a.partial = partial;
     a.d_pos = d_pos;
     a.n_heads = n_heads;
     a.n_kv_heads = n_kv_heads;
@@ -2424,39 +2465,46 @@ extern "C" void hbm_stream_probe(void *dst, const void *a, const void *b, size_t
     LAUNCH_OK();
 }
 
-// The device's read peak: a grid-stride read of n16 chunks with four non-temporal 16-byte loads
-// in flight per thread, any launch shape. The xor of what a thread read is stored only if it
-// equals a constant no random buffer is expected to produce, so the loads stay live without a
-// write stream.
+// The device read peak (bench/bandwidth.cu:25-116 read_kernel): a grid-stride read of 16-byte
+// chunks, U non-temporal loads in flight per thread per round; the xor of the data is stored only
+// in the unlikely case it equals a constant, so the loads are not removed.
+template <int U>
 __global__ __launch_bounds__(1024) void read_peak_kernel(const u32x4 *a, size_t n16,
                                                          uint32_t *out) {
     const size_t threads = (size_t)gridDim.x * blockDim.x;
     uint32_t acc = 0;
     for (size_t base = (size_t)blockIdx.x * blockDim.x + threadIdx.x; base < n16;
-         base += 4 * threads) {
-        u32x4 v[4];
+         base += U * threads) {
+        u32x4 v[U];
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
+        for (int u = 0; u < U; u++) {
             const size_t i = base + u * threads;
             v[u] = i < n16 ? __builtin_nontemporal_load(a + i) : u32x4{0, 0, 0, 0};
         }
 #pragma unroll
-        for (int u = 0; u < 4; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+        for (int u = 0; u < U; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
     }
     if (acc == 0x9e3779b9u) *out = acc;
 }
 
 extern "C" void hbm_read_peak_probe(unsigned *out, const void *a, size_t n_bytes, int blocks,
-                                    int threads, hipStream_t stream) {
+                                    int threads, int loads_in_flight, hipStream_t stream) {
     if (n_bytes % 16 != 0 || !aligned16(a) || out == nullptr || blocks < 1 ||
         blocks > (1 << 20) || (threads != 64 && threads != 128 && threads != 256 &&
-                               threads != 512 && threads != 1024)) {
+                               threads != 512 && threads != 1024) ||
+        (loads_in_flight != 4 && loads_in_flight != 8 && loads_in_flight != 16)) {
         llm_fail("hbm_read_peak_probe: %zu bytes (a multiple of 16, 16-byte aligned), %d blocks "
-                 "of %d threads (64..1024, a power of two)", n_bytes, blocks, threads);
+                 "of %d threads (64..1024, a power of two), %d loads in flight (4, 8 or 16)",
+                 n_bytes, blocks, threads, loads_in_flight);
         return;
     }
     if (n_bytes == 0) return;
-    read_peak_kernel<<<blocks, threads, 0, stream>>>((const u32x4 *)a, n_bytes / 16, out);
+    const u32x4 *p = (const u32x4 *)a;
+    switch (loads_in_flight) {
+    case 4: read_peak_kernel<4><<<blocks, threads, 0, stream>>>(p, n_bytes / 16, out); break;
+    case 8: read_peak_kernel<8><<<blocks, threads, 0, stream>>>(p, n_bytes / 16, out); break;
+    default: read_peak_kernel<16><<<blocks, threads, 0, stream>>>(p, n_bytes / 16, out); break;
+    }
     LAUNCH_OK();
 }
 

@@ -1,5 +1,5 @@
 // The whole decode step as one persistent kernel for gfx950: one workgroup of 8 waves per CU,
-// cooperatively launched (so all workgroups are resident), with no grid barrier. Each phase
+// all resident at once (the grid is the CU count, one workgroup per CU), with no grid barrier. Each phase
 // computes exactly what the standalone kernels compute (same per-row, per-head and per-block
 // arithmetic), so the step is bit-identical to the multi-kernel step it replaces
 // (src/forward.cu:118-193 order):
@@ -46,9 +46,6 @@ constexpr int PHASES = 5;                  // tagged vectors written per layer
 
 __device__ __forceinline__ uint64_t ld_coh64(const void *p) {
     return __hip_atomic_load(gptr((uint64_t *)p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ unsigned ld_coh_u32(const unsigned *p) {
-    return __hip_atomic_load(gptr((unsigned *)p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------- arguments
@@ -134,8 +131,9 @@ __device__ __forceinline__ const uint32_t *my_copy(const uint32_t *v) {
 // p = lane + 64 j): a wave with weight loads in flight would see the data only after them, since
 // vector loads complete in order, so the workgroups that prefetch weights leave polling to a
 // wave that has none. Otherwise every thread polls (p = threadIdx.x + THREADS j). The workgroup
-// syncs before (the previous contents of dst have been read) and after. Bounded: on timeout, or
-// once another wave has timed out, it sets the error flag and goes on with what it read.
+// syncs before (the previous contents of dst have been read) and after. Bounded: once the error
+// flag is set (an earlier error, or another wait that timed out), or when its own polls run out
+// (the flag then becomes 2 unless already set), it goes on with what it read.
 template <int PAIRS, bool ONE_WAVE, class Src>
 __device__ __forceinline__ void stage_pairs(Src src, uint32_t tag, uint32_t *dst, int *err) {
     constexpr int STEP = ONE_WAVE ? 64 : THREADS;
@@ -156,11 +154,7 @@ __device__ __forceinline__ void stage_pairs(Src src, uint32_t tag, uint32_t *dst
                          (uint32_t)((w[j] >> 32) & 0xffffu) == tag;
             }
             if (fresh) break;
-            if ((++spins & 63) == 0 &&
-                (spins > SPIN_LIMIT || ld_coh_u32((const unsigned *)err))) {
-                __hip_atomic_store(gptr(err), 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
-            }
+            if ((++spins & 63) == 0 && wait_gives_up(spins, SPIN_LIMIT, err)) break;
             if constexpr (POLL_SLEEP > 0) __builtin_amdgcn_s_sleep(POLL_SLEEP);
         }
 #pragma unroll
@@ -1152,12 +1146,8 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                     tw = __hip_atomic_load(gptr(a.token_word), __ATOMIC_RELAXED,
                                            __HIP_MEMORY_SCOPE_AGENT);
                     if ((uint32_t)tw == tag_of(seq_end)) break;
-                    if ((++spins & 63) == 0 &&
-                        (spins > SPIN_LIMIT || ld_coh_u32((const unsigned *)a.error_flag))) {
-                        __hip_atomic_store(gptr(a.error_flag), 2, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
+                    if ((++spins & 63) == 0 && wait_gives_up(spins, SPIN_LIMIT, a.error_flag))
                         break;
-                    }
                     __builtin_amdgcn_s_sleep(1);
                 }
                 const int t = (int)(tw >> 32);
@@ -1288,11 +1278,29 @@ int step_kernel_grid() {
     return cus > 1024 ? 1024 : cus;
 }
 
+// The workgroups wait for each other's tagged words, so all of them must be resident at once.
+// The grid is the CU count and one workgroup fits a CU (checked here with the runtime's
+// occupancy query), so a launch on an otherwise idle device places every workgroup at once; the
+// step's stream runs nothing beside it. Should a workgroup still start late (another process
+// holding CUs), the others' bounded waits let it catch up or end the step with the error flag
+// set, never a hang. A plain launch is used, not hipLaunchCooperativeKernel: its co-residency
+// check is the one made here, and under rocprofv3 the HIP runtime's exit-time release of the
+// cooperative launch's resources ran after the profiler had shut its HSA runtime down and
+// faulted (SIGSEGV in libhsa-runtime64, called from libamdhip64's exit handler, on a
+// device-mapped page), after every result had been written.
 bool step_kernel_launch(const Config *cfg, const StepArgs &args, int grid, hipStream_t stream) {
     const void *fn = step_kernel_for(cfg);
     if (!fn) return llm_fail("step kernel: no specialisation for these shapes");
     if (!step_grid_fits(cfg, grid)) return llm_fail("step kernel: grid of %d does not fit", grid);
+    int per_cu = 0, dev = 0, cus = 0;
+    if (!HIP_OK(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, THREADS, 0)) ||
+        !HIP_OK(hipGetDevice(&dev)) ||
+        !HIP_OK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)))
+        return false;
+    if ((long)per_cu * cus < grid)
+        return llm_fail("step kernel: %d workgroups cannot all be resident (%d per CU, %d CUs)",
+                        grid, per_cu, cus);
     StepArgs a = args;
     void *params[] = {&a};
-    return HIP_OK(hipLaunchCooperativeKernel(fn, dim3(grid), dim3(THREADS), params, 0, stream));
+    return HIP_OK(hipLaunchKernel(fn, dim3(grid), dim3(THREADS), params, 0, stream));
 }

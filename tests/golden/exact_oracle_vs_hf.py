@@ -5,6 +5,10 @@ mode (the HIP kernels' fp32 order, which the GPU step equals bit for bit) are te
 HF's tokens, and each step's 151936 logits are compared with HF's. This separates what any
 summation order loses to 28 layers of bf16 rounding from what the kernels' order adds.
 
+Writes tests/golden/exact_oracle_vs_hf.json: per full-logit step, each mode's max-abs difference
+from HF and the bf16 ulp of HF's largest |logit| in that row. The GPU step test holds the GPU's
+per-step max-abs to the EXACT mode's plus one such ulp.
+
 CPU only, about 5 minutes on 8 cores. Run from the repository root:
     python tests/golden/exact_oracle_vs_hf.py
 """
@@ -34,11 +38,14 @@ def main():
     prompt, ref = meta["prompt"], [int(x) for x in f["greedy"]]
     full_steps = [int(x) for x in f["full_steps"]]
     last = max(full_steps)
+    record = {"full_steps": full_steps, "source": "oracle teacher-forced on HF's tokens vs "
+              "tests/golden/hf_qwen3_06b_greedy.npz full_logits"}
     for mode, name in [(oracle.EXACT, "EXACT"), (oracle.GPU_ORDER, "GPU_ORDER")]:
         orc = oracle.Model(cfg, w, max_seq=len(prompt) + last + 8)
         for pos, tok in enumerate(prompt[:-1]):
             orc.forward(tok, pos, mode)
         tok, worst, over, ulps = prompt[-1], 0.0, 0, 0.0
+        per_step, units = [], []
         for i in range(last + 1):
             orc.forward(tok, len(prompt) - 1 + i, mode)
             if i in full_steps:
@@ -47,11 +54,18 @@ def main():
                 d = np.abs(lg - hf)
                 worst = max(worst, float(d.max()))
                 over += int(np.sum(d > 2e-2))
-                ulps = max(ulps, float(d.max()) / float(ulp_bf16(np.abs(hf).max())))
+                unit = float(ulp_bf16(np.abs(hf).max()))
+                ulps = max(ulps, float(d.max()) / unit)
+                per_step.append(float(d.max()))
+                units.append(unit)
             tok = ref[i]
         n = len(full_steps) * f["full_logits"].shape[1]
         print(f"{name}: max-abs {worst:.4f} over {n} logits at steps {full_steps}; {over} above "
               f"2e-2; at most {ulps:.2f} bf16 ulps of the row's largest logit", flush=True)
+        record[name] = {"max_abs_per_step": per_step, "max_abs": worst, "above_2e-2": over}
+        record["row_ulp_per_step"] = units
+    with open(os.path.join(HERE, "exact_oracle_vs_hf.json"), "w") as fh:
+        json.dump(record, fh, indent=1)
 
 
 if __name__ == "__main__":

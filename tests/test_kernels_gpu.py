@@ -494,6 +494,53 @@ def test_attention_rejects_a_workspace_too_small(gpu):
         dec.close()
 
 
+@pytest.mark.parametrize("hq,hkv,pos,max_seq", [(32, 8, 8447, 8448), (16, 8, 4095, 4096),
+                                                 (16, 8, 300, 4096)])
+def test_attention_reference_sized_att(gpu, oracle, hq, hkv, pos, max_seq):
+    """attention_forward with `att` allocated the reference's way (src/forward.cu:10-51: its own
+    hipMalloc of [n_heads, max_seq] floats, src/forward.cuh:13): the scores go there and the
+    block statistics and partial outputs to the library's own array. Bit-identical to the
+    oracle's GPU order; a call with the full workspace in between leaves the next reference-sized
+    call unaffected (every value it reads it wrote)."""
+    import ctypes
+    import torch
+    from llm_inference_amd import model
+    ident(f"attention reference-sized att {hq}/{hkv} pos{pos}")
+    rt = model._hip()
+    D = 128
+    nbytes = hq * max_seq * 4
+    ptr = ctypes.c_void_p()
+    assert rt.hipMalloc(ctypes.byref(ptr), ctypes.c_size_t(nbytes)) == 0
+    try:
+        base, size = ctypes.c_void_p(), ctypes.c_size_t()
+        assert rt.hipMemGetAddressRange(ctypes.byref(base), ctypes.byref(size), ptr) == 0
+        full = gpu.attention_workspace_floats(hq, D, max_seq) * 4
+        print(f"[case] att allocation {size.value} bytes; the full workspace needs {full}",
+              flush=True)
+        if (hq, max_seq) == (32, 8448):
+            assert size.value < full  # this case runs on the library's array
+        rng = np.random.default_rng(hq * 1000 + pos)
+        scale = float(np.float32(1.0 / np.sqrt(D)))
+        for rnd in range(2):
+            q = rand_bf16(rng, hq * D)
+            kc = rand_bf16(rng, (max_seq, hkv * D))
+            vc = rand_bf16(rng, (max_seq, hkv * D))
+            qd, kd, vd = dev(q), dev(kc), dev(vc)
+            out = dev(np.full(hq * D, 0x7FC1, np.uint16))
+            gpu.attention_forward(out, qd, kd, vd, ptr.value, hq, hkv, D, dev_i32([pos]),
+                                  max_seq, scale)
+            assert np.array_equal(host(out), oracle.attention(q, kc, vc, hq, hkv, D, pos, scale,
+                                                              oracle.GPU_ORDER)), rnd
+            if rnd == 0:  # the full-workspace form in between, on other data
+                att = torch.zeros(full // 4, dtype=torch.float32, device="cuda")
+                gpu.attention_forward(out, dev(rand_bf16(rng, hq * D)), kd, vd, att, hq, hkv, D,
+                                      dev_i32([pos // 2]), max_seq, scale)
+                host(out)
+    finally:
+        torch.cuda.synchronize()
+        rt.hipFree(ptr)
+
+
 def test_qk_norm_rope_attention_fused_rejects(gpu):
     """Shapes the kernels are not built for are refused with a message."""
     import torch
@@ -537,27 +584,31 @@ def test_hbm_stream_probe(gpu):
 
 def test_hbm_read_peak_probe(gpu):
     """The read-peak probe reads every chunk of its grid-stride walk: a buffer of zeros with the
-    magic word in one chunk of a late iteration (thread 5, third pass, fourth load) makes exactly
-    that thread store it; without it nothing is stored. Bad launch shapes are refused."""
+    magic word in one chunk of a late iteration (thread 5, third pass, last load) makes exactly
+    that thread store it; without it nothing is stored. Every loads-in-flight count; bad launch
+    shapes are refused."""
     import torch
     ident("hbm_read_peak_probe")
     magic = 0x9e3779b9 - (1 << 32)  # as int32
-    for blocks, threads in [(3, 256), (2, 1024), (7, 64)]:
-        T = blocks * threads
-        n16 = 4 * T * 3 + 7
-        a = torch.zeros(n16 * 4, dtype=torch.int32, device="cuda")
-        out = torch.zeros(1, dtype=torch.int32, device="cuda")
-        gpu.hbm_read_peak_probe(out, a, n16 * 16, blocks, threads)
-        torch.cuda.synchronize()
-        assert int(out.item()) == 0
-        a[4 * (4 * T * 2 + 3 * T + 5)] = magic
-        gpu.hbm_read_peak_probe(out, a, n16 * 16, blocks, threads)
-        torch.cuda.synchronize()
-        assert int(out.item()) == magic
+    for U in (4, 8, 16):
+        for blocks, threads in [(3, 256), (2, 1024), (7, 64)]:
+            T = blocks * threads
+            n16 = U * T * 3 + 7
+            a = torch.zeros(n16 * 4, dtype=torch.int32, device="cuda")
+            out = torch.zeros(1, dtype=torch.int32, device="cuda")
+            gpu.hbm_read_peak_probe(out, a, n16 * 16, blocks, threads, U)
+            torch.cuda.synchronize()
+            assert int(out.item()) == 0, (U, blocks, threads)
+            a[4 * (U * T * 2 + (U - 1) * T + 5)] = magic
+            gpu.hbm_read_peak_probe(out, a, n16 * 16, blocks, threads, U)
+            torch.cuda.synchronize()
+            assert int(out.item()) == magic, (U, blocks, threads)
     with pytest.raises(gpu.LlmError):
         gpu.hbm_read_peak_probe(out, a, 64, 4, 100)
     with pytest.raises(gpu.LlmError):
         gpu.hbm_read_peak_probe(out, a, 24, 4, 256)
+    with pytest.raises(gpu.LlmError):
+        gpu.hbm_read_peak_probe(out, a, 64, 4, 256, 6)
 
 
 # ---------------------------------------------------------------- temperature sampling

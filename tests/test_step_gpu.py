@@ -258,12 +258,12 @@ def test_qwen3_06b_greedy_256_vs_hf_fixture(gpu):
     these steps, so no summation order meets 2e-2 everywhere. At the fixture's 9 full-vocabulary
     steps (0, 32, ..., 224, 255) every one of the 151936 logits is compared: the max-abs
     difference is printed against the 2e-2 logit bound (with the count of logits above it), and
-    every logit must be within 4 bf16 ulps, in units of the row's largest logit, of HF's value (a
-    logit's error comes from the final hidden vector's, on the scale of the row). The oracle's
-    exact mode, teacher-forced the same way, is itself 0.0518 (3.31 such ulps) from HF over these
-    logits, with 44525 of them beyond 2e-2 (tests/golden/exact_oracle_vs_hf.py): that bound is
-    below what 28 layers of bf16 rounding leave any summation order. (With N(0, 0.02) weights the logits are flat: most steps are near ties, where
-    either token is a correct greedy choice, ref/greedy.py:14-31.)"""
+    at every such step the GPU's max-abs difference from HF may exceed the exact mode's (the
+    oracle teacher-forced the same way, tests/golden/exact_oracle_vs_hf.json, written by
+    exact_oracle_vs_hf.py) by at most one bf16 ulp of the row's largest logit: the GPU is as
+    close to HF as exact arithmetic is, step by step. (With N(0, 0.02) weights the logits are
+    flat: most steps are near ties, where either token is a correct greedy choice,
+    ref/greedy.py:14-31.)"""
     import json
     import os
     from llm_inference_amd import model
@@ -272,6 +272,9 @@ def test_qwen3_06b_greedy_256_vs_hf_fixture(gpu):
     f = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
                              "hf_qwen3_06b_greedy.npz"))
     meta = json.loads(str(f["meta"]))
+    with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                           "exact_oracle_vs_hf.json")) as fh:
+        rel = json.load(fh)
     ref = [int(x) for x in f["greedy"]]
     cfg = model.qwen3_config("0.6B", max_seq_len=len(meta["prompt"]) + len(ref) + 8)
     dec = model.Decoder(cfg, ("synth", 0, 0.02, 0.1))
@@ -284,7 +287,9 @@ def test_qwen3_06b_greedy_256_vs_hf_fixture(gpu):
         decided = agree = 0
         worst = 0.0
         full_steps = [int(x) for x in f["full_steps"]]
+        assert rel["full_steps"] == full_steps
         full_worst, full_ulps, full_over = 0.0, 0, 0
+        beyond_exact = []  # per full step: GPU max-abs - exact mode's, in row ulps
         for i in range(len(ref)):
             got = dec.sample_argmax()
             lg = bf16_vals(dec.logits()).astype(np.float64)
@@ -302,6 +307,12 @@ def test_qwen3_06b_greedy_256_vs_hf_fixture(gpu):
                 # of the final hidden vector, on the scale of the row, not of its own value
                 unit = float(ulp_bf16(np.abs(hf_all).max()))
                 full_ulps = max(full_ulps, float(d_all.max()) / unit)
+                j = full_steps.index(i)
+                assert unit == rel["row_ulp_per_step"][j], i
+                beyond_exact.append((float(d_all.max()) - rel["EXACT"]["max_abs_per_step"][j])
+                                    / unit)
+                assert float(d_all.max()) <= rel["EXACT"]["max_abs_per_step"][j] + unit, \
+                    (i, float(d_all.max()), rel["EXACT"]["max_abs_per_step"][j], unit)
             if f["greedy_gap"][i] > 0.07:
                 decided += 1
                 agree += got == ref[i]
@@ -313,8 +324,8 @@ def test_qwen3_06b_greedy_256_vs_hf_fixture(gpu):
         print(f"[case] all {f['full_logits'].shape[1]} logits at steps {full_steps}: max-abs "
               f"{full_worst:.4f} (logit bound 2e-2), {full_over} of "
               f"{len(full_steps) * f['full_logits'].shape[1]} logits above 2e-2, at most "
-              f"{full_ulps:.2f} bf16 ulps of the row's largest logit", flush=True)
-        assert full_ulps <= 4, full_ulps
+              f"{full_ulps:.2f} bf16 ulps of the row's largest logit; beyond the exact "
+              f"mode's max-abs by at most {max(beyond_exact):.2f} such ulps (bound 1)", flush=True)
     finally:
         dec.close()
 
@@ -686,6 +697,79 @@ def test_persistent_step_long_context(qwen06b, oracle):
                               orc.bufs["key_cache"].reshape(k.shape)[:, 5000].reshape(-1))
         assert np.array_equal(vv[:, 5000].reshape(-1),
                               orc.bufs["value_cache"].reshape(v.shape)[:, 5000].reshape(-1))
+    finally:
+        dec.close()
+
+
+@pytest.mark.parametrize("size", ["1.7B", "4B"])
+def test_persistent_step_wide_shapes_long_history(gpu, oracle, size):
+    """The 1.7B and 4B specialisations of the persistent step (2 and 4 query heads per kv head)
+    where the bench and STEP_AUTO run them: single positions 260 (five 64-position blocks) and
+    447 (seven; the last 4B position before the switch to the hipGraph) after a KV cache filled
+    with N(0, 1) below them, at full widths with 2 layers. Logits, argmax and the KV rows written
+    bit-identical to the oracle; then an 8-token generate from 440 in one launch."""
+    ident(f"persistent step {size} widths at positions 260 and 447")
+    from llm_inference_amd import model
+    cfg = model.qwen3_config(size, n_layers=2, max_seq_len=512)
+    dec = model.Decoder(cfg, ("synth", 31, 0.02, 0.1))
+    try:
+        rng = np.random.default_rng(447)
+        kvd = cfg.n_kv_heads * cfg.head_dim
+        k = rand_bf16(rng, (cfg.n_layers, 512, kvd))
+        v = rand_bf16(rng, (cfg.n_layers, 512, kvd))
+        dec.set_kv_cache(k, v)
+        w = dec.host_weights()
+        orc = oracle.Model(oracle_cfg(cfg), w, max_seq=512)
+        del w
+        orc.bufs["key_cache"][:] = k.reshape(-1)
+        orc.bufs["value_cache"][:] = v.reshape(-1)
+        dec.capture_graph("persistent")
+        assert dec.persistent
+        for pos in (260, 447):
+            tok = int(rng.integers(0, cfg.vocab_size))
+            dec.forward(tok, pos)
+            nxt = dec.sample_argmax()
+            ref = orc.forward(tok, pos, oracle.GPU_ORDER)
+            assert np.array_equal(dec.logits(), orc.logits), pos
+            assert nxt == ref, pos
+            kk, vv = dec.kv_cache()
+            ok = orc.bufs["key_cache"].reshape(k.shape)
+            ov = orc.bufs["value_cache"].reshape(v.shape)
+            assert np.array_equal(kk[:, pos], ok[:, pos]), pos
+            assert np.array_equal(vv[:, pos], ov[:, pos]), pos
+        got = dec.generate_greedy(nxt, 440, 8)
+        t, want = nxt, []
+        for i in range(8):
+            t = orc.forward(t, 440 + i, oracle.GPU_ORDER)
+            want.append(t)
+        assert got == want
+    finally:
+        dec.close()
+
+
+@pytest.mark.parametrize("mode", ["graph", "persistent"])
+def test_step_keeps_an_earlier_error_code(gpu, mode):
+    """A wait between workgroups that finds the error flag already set stops at once and leaves
+    the code alone: with the flag set to 1 (token or position out of range) from the host before
+    a step whose attention waits on other workgroups (graph step: the PV + combine launch at
+    position 200, four blocks; persistent step: every tagged-vector poll), the error reported
+    afterwards is the out-of-range one, not a timed-out wait. Every wait ends at once, so the
+    kernels exit normally."""
+    ident(f"earlier error code kept ({mode} step)")
+    from llm_inference_amd import LlmError, model
+    cfg = model.make_config(hidden_size=512, intermediate_size=1024, n_layers=2, n_heads=8,
+                            n_kv_heads=4, vocab_size=3000, max_seq_len=256)
+    dec = model.Decoder(cfg, ("synth", 9, 0.02, 0.1))
+    try:
+        dec.capture_graph(mode)
+        assert dec.persistent == (mode == "persistent")
+        model.copy_to_device(dec.s.error_flag, np.array([1], np.int32), 4)
+        dec.forward(17, 200)
+        with pytest.raises(LlmError, match="out of range"):
+            dec.sample_argmax()
+        # the flag was reported and cleared: the next step runs normally
+        dec.forward(17, 200)
+        assert 0 <= dec.sample_argmax() < cfg.vocab_size
     finally:
         dec.close()
 

@@ -9,8 +9,6 @@ import pytest
 
 from conftest import load_package, rand_bf16
 
-pytestmark = pytest.mark.gpu
-
 
 def _dev(bits):
     import torch
@@ -23,6 +21,7 @@ def _host(t):
     return t.cpu().numpy().view(np.uint16)
 
 
+@pytest.mark.gpu
 @pytest.mark.parametrize("first,second", [
     ((32, 8, 8447, 8448), (16, 8, 300, 512)),   # 4B heads at an 8192+ history, then 0.6B heads
     ((16, 8, 4095, 4096), (8, 2, 63, 64)),
@@ -55,7 +54,7 @@ def test_attention_noalloc_matches_attention_forward(gpu, first, second):
 
 def test_attention_noalloc_size_limit():
     """More workspace than the library's array holds is an error before anything is launched
-    (host-side; runs without a GPU too)."""
+    (host-side: runs in the CPU suite, no GPU call is made)."""
     pkg = load_package()
     L = pkg.lib()
     L.llm_clear_error()
