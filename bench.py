@@ -515,7 +515,23 @@ def phase_trace(positions=range(8, 40), size="0.6B"):
     trace = torch.zeros(n_stamps, dtype=torch.int64, device="cuda")
     dec.s.step_trace = ctypes.cast(ctypes.c_void_p(trace.data_ptr()),
                                    ctypes.POINTER(ctypes.c_longlong))
-    tok, stamps, layer_us, lm_us, step_us = 11, [], [], [], []
+    # rows per matrix workgroup (8 waves each, HQ attention workgroups own none): the rows of
+    # the kernel's phase_rows, to know which workgroups take part in a phase
+    waves = (grid - hq) * 8
+
+    def owners(R, min_per=1):
+        per = max(-(-R // waves), min_per)
+        return [b for b in range(hq, grid) if (b - hq) * 8 * per < R]
+
+    qd, kvd = hq * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
+    part = {"q/k/v rows (RMSNorm + GEMV)": (0, owners(qd + 2 * kvd, 4)),
+            "attention (one head per workgroup)": (0, list(range(hq))),
+            "o rows + residual": (1, owners(cfg.hidden_size)),
+            "gate/up rows + SwiGLU (RMSNorm + GEMV)": (2, owners(cfg.intermediate_size)),
+            "down rows + residual": (3, owners(cfg.hidden_size))}
+    rows = {k: {"staged": [], "stored_median": [], "stored_max": []} for k in part}
+    layer_us, lm_us, step_us = [], [], []
+    tok = 11
     for pos in range(max(positions) + 1):
         trace.zero_()
         torch.cuda.synchronize()
@@ -524,33 +540,18 @@ def phase_trace(positions=range(8, 40), size="0.6B"):
         if pos not in positions:
             continue
         t = trace.cpu().numpy().astype(np.int64)
-        stamps.append(t[4 * nl + 3:].reshape(grid, 8))
+        per_wg = t[4 * nl + 3:].reshape(grid, 8)
+        t0 = per_wg[part["q/k/v rows (RMSNorm + GEMV)"][1], 0].min()
+        for name, (ph, wgs) in part.items():
+            st = (per_wg[wgs, 2 * ph] - t0) / 100.0  # 100 MHz ticks -> us
+            sd = (per_wg[wgs, 2 * ph + 1] - t0) / 100.0
+            rows[name]["staged"].append(np.median(st))
+            rows[name]["stored_median"].append(np.median(sd))
+            rows[name]["stored_max"].append(sd.max())
         starts = t[[1 + 4 * l for l in range(nl)]]
         layer_us.append(np.diff(starts).mean() / 100.0)
         lm_us.append((t[2 + 4 * nl] - t[1 + 4 * nl]) / 100.0)  # LM head input staged -> end
         step_us.append((t[2 + 4 * nl] - t[0]) / 100.0)
-    # A workgroup takes part in a phase when its stamps of it are apart: one without rows there
-    # stamps "staged" and "stored" back to back (median over the positions, 100 MHz ticks)
-    per = np.stack(stamps)
-    dur = np.median(per[:, :, 1::2] - per[:, :, 0::2], axis=0) / 100.0  # [grid, phase]
-    wgs = np.arange(grid)
-
-    def takers(ph, attention):
-        return list(wgs[(dur[:, ph] > 0.15) & ((wgs < hq) == attention)])
-    part = {"q/k/v rows (RMSNorm + GEMV)": (0, takers(0, False)),
-            "attention (one head per workgroup)": (0, list(range(hq))),
-            "o rows + residual": (1, list(wgs[dur[:, 1] > 0.15])),
-            "gate/up rows + SwiGLU (RMSNorm + GEMV)": (2, list(wgs[dur[:, 2] > 0.15])),
-            "down rows + residual": (3, list(wgs[dur[:, 3] > 0.15]))}
-    rows = {k: {"staged": [], "stored_median": [], "stored_max": []} for k in part}
-    for per_wg in stamps:
-        t0 = per_wg[part["q/k/v rows (RMSNorm + GEMV)"][1], 0].min()
-        for name, (ph, ws) in part.items():
-            st = (per_wg[ws, 2 * ph] - t0) / 100.0  # 100 MHz ticks -> us
-            sd = (per_wg[ws, 2 * ph + 1] - t0) / 100.0
-            rows[name]["staged"].append(np.median(st))
-            rows[name]["stored_median"].append(np.median(sd))
-            rows[name]["stored_max"].append(sd.max())
     dec.close()
     out = {k: {m: round(float(np.median(v)), 2) for m, v in r.items()} for k, r in rows.items()}
     out["layer_us"] = round(float(np.median(layer_us)), 2)

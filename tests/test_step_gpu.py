@@ -782,8 +782,9 @@ def test_graph_step_4b_after_8192_positions(gpu, oracle, attn):
     argmax bit-identical to the oracle's GPU order at positions 8192-8199 (each step's KV rows
     written past the reference's 4096-slot cap and read back by the next), then a one-call
     generate_greedy of 8 tokens from 8200 equal to the oracle's. Every attention form of the
-    step: QK-norm + RoPE + attention in one launch (the default at this length), QK-norm + RoPE
-    inside the attention's scores pass, and qk_norm_rope_forward + attention_forward."""
+    step: QK-norm + RoPE + attention in one launch (ATTN_ONE_PASS, opt-in), QK-norm + RoPE inside
+    the attention's scores pass (what ATTN_AUTO takes at these shapes), and qk_norm_rope_forward
+    + attention_forward."""
     ident(f"4B graph step from 8192 positions, {attn} attention")
     from llm_inference_amd import model
     cfg = model.qwen3_config("4B", n_layers=2, max_seq_len=8448)
