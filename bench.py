@@ -12,7 +12,7 @@ tokens / the region's seconds, `ms_per_step` the region's milliseconds per step.
 The JSON line also carries:
   device_peak   the device's copy and read bandwidth as the reference measures them beside every
                 run (bench/bandwidth.cu: a 1 GiB device-to-device copy, median of 20 after 200
-                warm-ups; a 1 GiB read, median of 20, best of 45 launch shapes)
+                warm-ups; a 4 GiB read, median of 20, best of 96 launch shapes)
   roofline      the dominant kernel: the persistent step kernel (ONE launch decodes a step's 256
                 tokens: all layers, the LM head and the argmax, the argmax fed to the next token
                 inside the kernel), timed with HIP events on the step's stream (mean over the
@@ -91,15 +91,12 @@ def rotating(n_bytes_each, min_total=512 << 20, max_copies=64):
 def device_peak(pkg, stream):
     """The device's copy and read bandwidth, measured as bench/bandwidth.cu:25-116 does: a
     1 GiB device-to-device copy (median of 20 after 200 warm-ups; a copy moves 2x the bytes),
-    then a 1 GiB read (hbm_read_peak_probe), median of 20 after 3 warm-ups per launch shape,
-    the best of 3 workgroup sizes x 5 workgroups-per-CU counts x 3 loads-in-flight counts."""
+    then a 4 GiB read (hbm_read_peak_probe), median of 20 after 3 warm-ups per launch shape,
+    the best of 4 workgroup sizes x 4 workgroups-per-CU counts x 3 loads-in-flight counts x 2
+    layouts (grid-stride; one range per workgroup, keys ending in c). The read is 4 GiB so that
+    a launch's fixed cost (a few microseconds) is under 1% of its ~0.6 ms."""
     import torch
-    nbytes = 1 << 30
     L = pkg.lib()
-    src = torch.empty(nbytes // 2, dtype=torch.int16, device="cuda")
-    L.synth_fill(src.data_ptr(), src.numel(), 321, 0, 0.0, 1.0, stream)
-    dst = torch.empty_like(src)
-    out = torch.zeros(1, dtype=torch.int32, device="cuda")
     ts = torch.cuda.ExternalStream(stream)
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
 
@@ -114,26 +111,39 @@ def device_peak(pkg, stream):
                 ms.append(ev0.elapsed_time(ev1))
         return statistics.median(ms)
 
+    copy_bytes, read_bytes = 1 << 30, 4 << 30
+    src = torch.empty(copy_bytes // 2, dtype=torch.int16, device="cuda")
+    L.synth_fill(src.data_ptr(), src.numel(), 321, 0, 0.0, 1.0, stream)
+    dst = torch.empty_like(src)
     with torch.cuda.stream(ts):
         copy_ms = median_ms(lambda: dst.copy_(src), 200, 20)
-    copy_gbs = 2 * nbytes / (copy_ms * 1e-3) / 1e9
-    cus = torch.cuda.get_device_properties(0).multi_processor_count
-    shapes = {}
-    for loads in (4, 8, 16):
-        for threads in (256, 512, 1024):
-            for per_cu in (1, 2, 4, 8, 16):
-                blocks = per_cu * cus
-                ms = median_ms(lambda: pkg.hbm_read_peak_probe(out, src, nbytes, blocks, threads,
-                                                               loads, stream=stream), 3, 20)
-                shapes[f"{blocks}x{threads}x{loads}"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
-    best = max(shapes, key=shapes.get)
+    copy_gbs = 2 * copy_bytes / (copy_ms * 1e-3) / 1e9
     torch.cuda.synchronize()
     del src, dst
+    src = torch.empty(read_bytes // 2, dtype=torch.int16, device="cuda")
+    L.synth_fill(src.data_ptr(), src.numel(), 321, 0, 0.0, 1.0, stream)
+    out = torch.zeros(1, dtype=torch.int32, device="cuda")
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    shapes = {}
+    for contiguous in (0, 1):
+        for loads in (4, 8, 16):
+            for threads in (128, 256, 512, 1024):
+                for per_cu in (1, 2, 4, 8):
+                    blocks = per_cu * cus
+                    ms = median_ms(lambda: pkg.hbm_read_peak_probe(
+                        out, src, read_bytes, blocks, threads, loads, contiguous, stream=stream),
+                        3, 20)
+                    key = f"{blocks}x{threads}x{loads}" + ("c" if contiguous else "")
+                    shapes[key] = round(read_bytes / (ms * 1e-3) / 1e9, 1)
+    best = max(shapes, key=shapes.get)
+    torch.cuda.synchronize()
+    del src
     res = {"copy_GB/s": round(copy_gbs, 1), "read_GB/s": shapes[best], "read_best_shape": best,
-           "read_shapes_GB/s": shapes, "bytes": nbytes,
+           "read_shapes_GB/s": shapes, "copy_bytes": copy_bytes, "read_bytes": read_bytes,
            "method": "bench/bandwidth.cu: 1 GiB D2D copy (2x bytes), median of 20 after 200 "
-                     "warm-ups; 1 GiB read, median of 20, best of 45 launch shapes "
-                     "(workgroups x threads x 16-byte loads in flight per thread)"}
+                     "warm-ups; 4 GiB read, median of 20, best of 96 launch shapes "
+                     "(workgroups x threads x 16-byte loads in flight per thread, grid-stride "
+                     "or a range per workgroup: c)"}
     log(f"device peak: copy {res['copy_GB/s']} GB/s, read {res['read_GB/s']} GB/s ({best})")
     return res
 

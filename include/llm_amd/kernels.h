@@ -162,10 +162,12 @@ void hbm_stream_probe(void *dst, const void *a, const void *b, size_t n_bytes, i
  * (bench/bandwidth.cu:25-116 read_kernel: a grid-stride read, the best of several launch
  * shapes). Reads n_bytes of a (n_bytes % 16 == 0, 16-byte aligned) with `blocks` workgroups of
  * `threads` threads (64..1024, a power of two), each thread keeping loads_in_flight (4, 8 or 16)
- * non-temporal 16-byte loads in flight per round; *out is written only in the unlikely case the
- * xor of a thread's data equals 0x9e3779b9. */
+ * non-temporal 16-byte loads in flight per round; contiguous 0 walks the buffer grid-stride (the
+ * reference's pattern), 1 gives each workgroup one contiguous range (as a GEMV's workgroups read
+ * their rows). *out is written only in the unlikely case the xor of a thread's data equals
+ * 0x9e3779b9. */
 void hbm_read_peak_probe(unsigned *out, const void *a, size_t n_bytes, int blocks, int threads,
-                         int loads_in_flight, hipStream_t stream);
+                         int loads_in_flight, int contiguous, hipStream_t stream);
 
 /* No counterpart in the reference. Decode attention as attention_forward computes it, without
  * the `att` argument, for callers that cannot allocate device memory (code under stream

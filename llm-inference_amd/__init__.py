@@ -74,7 +74,7 @@ _SIGS = {
     "rmsnorm_gemv_forward": (None, [_vp] * 4 + [_f, _i, _i, _vp]),
     "rmsnorm_gate_up_forward": (None, [_vp] * 5 + [_f, _i, _i, _vp]),
     "hbm_stream_probe": (None, [_vp, _vp, _vp, _sz, _i, _vp]),
-    "hbm_read_peak_probe": (None, [_vp, _vp, _sz, _i, _i, _i, _vp]),
+    "hbm_read_peak_probe": (None, [_vp, _vp, _sz, _i, _i, _i, _i, _vp]),
     "qk_norm_rope_attention_forward": (None, [_vp] * 9 + [_vp, _i, _i, _i, _f, _f, _i, _f, _vp]),
     "qk_norm_rope_attention_one_pass": (None, [_vp] * 11 + [_i, _i, _i, _f, _f, _i, _f, _vp]),
     "attention_one_pass_bytes": (_sz, [_i, _i, _i]),
@@ -295,12 +295,14 @@ def hbm_stream_probe(dst, a, b, n_bytes, mode, stream=None):
     _call(lib().hbm_stream_probe, _ptr(dst), _ptr(a), _ptr(b), n_bytes, mode, _stream(stream))
 
 
-def hbm_read_peak_probe(out, a, n_bytes, blocks, threads, loads_in_flight=4, stream=None):
+def hbm_read_peak_probe(out, a, n_bytes, blocks, threads, loads_in_flight=4, contiguous=0,
+                        stream=None):
     """Reads n_bytes of `a` with `blocks` workgroups of `threads` threads, loads_in_flight
-    16-byte loads per thread per round (the read-peak probe); `out` is a device word written
-    only if a thread's xor equals 0x9e3779b9."""
+    16-byte loads per thread per round, grid-stride (contiguous=0) or one range per workgroup
+    (contiguous=1) (the read-peak probe); `out` is a device word written only if a thread's xor
+    equals 0x9e3779b9."""
     _call(lib().hbm_read_peak_probe, _ptr(out), _ptr(a), n_bytes, blocks, threads,
-          loads_in_flight, _stream(stream))
+          loads_in_flight, contiguous, _stream(stream))
 
 
 def sample_forward(out, x, n, inv_temp, u, stream=None):

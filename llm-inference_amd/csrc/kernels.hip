@@ -2465,21 +2465,30 @@ extern "C" void hbm_stream_probe(void *dst, const void *a, const void *b, size_t
     LAUNCH_OK();
 }
 
-// The device read peak (bench/bandwidth.cu:25-116 read_kernel): a grid-stride read of 16-byte
-// chunks, U non-temporal loads in flight per thread per round; the xor of the data is stored only
-// in the unlikely case it equals a constant, so the loads are not removed.
-template <int U>
+// The device read peak (bench/bandwidth.cu:25-116 read_kernel): 16-byte chunks, U non-temporal
+// loads in flight per thread per round, either grid-stride over the whole buffer (CONTIG false,
+// the reference's pattern) or over one contiguous range per workgroup (CONTIG true, as a GEMV's
+// workgroups read their rows). The xor of the data is stored only in the unlikely case it equals
+// a constant, so the loads are not removed.
+template <int U, bool CONTIG>
 __global__ __launch_bounds__(1024) void read_peak_kernel(const u32x4 *a, size_t n16,
                                                          uint32_t *out) {
-    const size_t threads = (size_t)gridDim.x * blockDim.x;
+    size_t first = 0, end = n16, stride = (size_t)gridDim.x * blockDim.x;
+    size_t t0 = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if constexpr (CONTIG) {
+        const size_t span = (n16 + gridDim.x - 1) / gridDim.x;
+        first = min(n16, (size_t)blockIdx.x * span);
+        end = min(n16, first + span);
+        stride = blockDim.x;
+        t0 = first + threadIdx.x;
+    }
     uint32_t acc = 0;
-    for (size_t base = (size_t)blockIdx.x * blockDim.x + threadIdx.x; base < n16;
-         base += U * threads) {
+    for (size_t base = t0; base < end; base += U * stride) {
         u32x4 v[U];
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const size_t i = base + u * threads;
-            v[u] = i < n16 ? __builtin_nontemporal_load(a + i) : u32x4{0, 0, 0, 0};
+            const size_t i = base + u * stride;
+            v[u] = i < end ? __builtin_nontemporal_load(a + i) : u32x4{0, 0, 0, 0};
         }
 #pragma unroll
         for (int u = 0; u < U; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
@@ -2488,23 +2497,33 @@ __global__ __launch_bounds__(1024) void read_peak_kernel(const u32x4 *a, size_t 
 }
 
 extern "C" void hbm_read_peak_probe(unsigned *out, const void *a, size_t n_bytes, int blocks,
-                                    int threads, int loads_in_flight, hipStream_t stream) {
+                                    int threads, int loads_in_flight, int contiguous,
+                                    hipStream_t stream) {
     if (n_bytes % 16 != 0 || !aligned16(a) || out == nullptr || blocks < 1 ||
         blocks > (1 << 20) || (threads != 64 && threads != 128 && threads != 256 &&
                                threads != 512 && threads != 1024) ||
-        (loads_in_flight != 4 && loads_in_flight != 8 && loads_in_flight != 16)) {
+        (loads_in_flight != 4 && loads_in_flight != 8 && loads_in_flight != 16) ||
+        (contiguous != 0 && contiguous != 1)) {
         llm_fail("hbm_read_peak_probe: %zu bytes (a multiple of 16, 16-byte aligned), %d blocks "
-                 "of %d threads (64..1024, a power of two), %d loads in flight (4, 8 or 16)",
-                 n_bytes, blocks, threads, loads_in_flight);
+                 "of %d threads (64..1024, a power of two), %d loads in flight (4, 8 or 16), "
+                 "layout %d (0 grid-stride, 1 a range per workgroup)",
+                 n_bytes, blocks, threads, loads_in_flight, contiguous);
         return;
     }
     if (n_bytes == 0) return;
     const u32x4 *p = (const u32x4 *)a;
-    switch (loads_in_flight) {
-    case 4: read_peak_kernel<4><<<blocks, threads, 0, stream>>>(p, n_bytes / 16, out); break;
-    case 8: read_peak_kernel<8><<<blocks, threads, 0, stream>>>(p, n_bytes / 16, out); break;
-    default: read_peak_kernel<16><<<blocks, threads, 0, stream>>>(p, n_bytes / 16, out); break;
+    const size_t n16 = n_bytes / 16;
+#define PEAK(U, C) read_peak_kernel<U, C><<<blocks, threads, 0, stream>>>(p, n16, out)
+    if (contiguous) {
+        if (loads_in_flight == 4) PEAK(4, true);
+        else if (loads_in_flight == 8) PEAK(8, true);
+        else PEAK(16, true);
+    } else {
+        if (loads_in_flight == 4) PEAK(4, false);
+        else if (loads_in_flight == 8) PEAK(8, false);
+        else PEAK(16, false);
     }
+#undef PEAK
     LAUNCH_OK();
 }
 

@@ -74,7 +74,14 @@ float orc_bf16_to_f32(uint16_t b) {
 
 float orc_round_bf16(float f) { return orc_bf16_to_f32(orc_f32_to_bf16(f)); }
 
-static inline float bf(uint16_t b) { return orc_bf16_to_f32(b); }
+/* The same conversion as orc_bf16_to_f32, inlined where the hot loops use it (the exported
+ * function is called through the PLT in a shared library and would not be inlined). */
+static inline float bf(uint16_t b) {
+    uint32_t u = (uint32_t)b << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
 static inline uint16_t tobf(float f) { return orc_f32_to_bf16(f); }
 
 /* ------------------------------------------------------------------------------------------ */
@@ -184,15 +191,18 @@ static float tree_sum(float *a, int n) {
 }
 
 /* A 64-lane wave: lane l takes 8-element chunks l, l+64, ...; each lane fma-accumulates its
- * elements in order; the lanes then meet in the xor tree. cols % 8 == 0. */
+ * elements in order; the lanes then meet in the xor tree. cols % 8 == 0. The loops run the 64
+ * lanes' chains side by side (the same operations in each lane's order), so the CPU overlaps
+ * 64 independent fma chains instead of waiting out one at a time. */
 static float dot_gpu(const uint16_t *w, const uint16_t *x, int cols) {
     float acc[64];
+    for (int l = 0; l < 64; l++) acc[l] = 0.0f;
     int n_chunks = cols / 8;
-    for (int l = 0; l < 64; l++) {
-        float a = 0.0f;
-        for (int c = l; c < n_chunks; c += 64)
-            for (int e = 0; e < 8; e++) a = fmaf(bf(w[8 * c + e]), bf(x[8 * c + e]), a);
-        acc[l] = a;
+    for (int c0 = 0; c0 < n_chunks; c0 += 64) {
+        int lanes = n_chunks - c0 < 64 ? n_chunks - c0 : 64;
+        const uint16_t *wc = w + 8 * c0, *xc = x + 8 * c0;
+        for (int e = 0; e < 8; e++)
+            for (int l = 0; l < lanes; l++) acc[l] = fmaf(bf(wc[8 * l + e]), bf(xc[8 * l + e]), acc[l]);
     }
     return tree_sum(acc, 64);
 }

@@ -583,32 +583,42 @@ def test_hbm_stream_probe(gpu):
 
 
 def test_hbm_read_peak_probe(gpu):
-    """The read-peak probe reads every chunk of its grid-stride walk: a buffer of zeros with the
-    magic word in one chunk of a late iteration (thread 5, third pass, last load) makes exactly
-    that thread store it; without it nothing is stored. Every loads-in-flight count; bad launch
-    shapes are refused."""
+    """The read-peak probe reads every chunk of its walk: a buffer of zeros with the magic word in
+    one chunk of a late round (grid-stride: thread 5, third pass, last load; one range per
+    workgroup: workgroup 1's thread 5, third pass, last load) makes exactly that thread store
+    it; without it nothing is stored. Every loads-in-flight count and both layouts, with a
+    length that is not a multiple of the grid; bad launch shapes are refused."""
     import torch
     ident("hbm_read_peak_probe")
     magic = 0x9e3779b9 - (1 << 32)  # as int32
-    for U in (4, 8, 16):
-        for blocks, threads in [(3, 256), (2, 1024), (7, 64)]:
-            T = blocks * threads
-            n16 = U * T * 3 + 7
-            a = torch.zeros(n16 * 4, dtype=torch.int32, device="cuda")
-            out = torch.zeros(1, dtype=torch.int32, device="cuda")
-            gpu.hbm_read_peak_probe(out, a, n16 * 16, blocks, threads, U)
-            torch.cuda.synchronize()
-            assert int(out.item()) == 0, (U, blocks, threads)
-            a[4 * (U * T * 2 + (U - 1) * T + 5)] = magic
-            gpu.hbm_read_peak_probe(out, a, n16 * 16, blocks, threads, U)
-            torch.cuda.synchronize()
-            assert int(out.item()) == magic, (U, blocks, threads)
+    for contiguous in (0, 1):
+        for U in (4, 8, 16):
+            for blocks, threads in [(3, 256), (2, 1024), (7, 64)]:
+                T = blocks * threads
+                if contiguous:
+                    span = U * threads * 3
+                    n16 = blocks * span - 5  # the last workgroup's range is short
+                    hit = span + U * threads * 2 + (U - 1) * threads + 5
+                else:
+                    n16 = U * T * 3 + 7
+                    hit = U * T * 2 + (U - 1) * T + 5
+                a = torch.zeros(n16 * 4, dtype=torch.int32, device="cuda")
+                out = torch.zeros(1, dtype=torch.int32, device="cuda")
+                gpu.hbm_read_peak_probe(out, a, n16 * 16, blocks, threads, U, contiguous)
+                torch.cuda.synchronize()
+                assert int(out.item()) == 0, (contiguous, U, blocks, threads)
+                a[4 * hit] = magic
+                gpu.hbm_read_peak_probe(out, a, n16 * 16, blocks, threads, U, contiguous)
+                torch.cuda.synchronize()
+                assert int(out.item()) == magic, (contiguous, U, blocks, threads)
     with pytest.raises(gpu.LlmError):
         gpu.hbm_read_peak_probe(out, a, 64, 4, 100)
     with pytest.raises(gpu.LlmError):
         gpu.hbm_read_peak_probe(out, a, 24, 4, 256)
     with pytest.raises(gpu.LlmError):
         gpu.hbm_read_peak_probe(out, a, 64, 4, 256, 6)
+    with pytest.raises(gpu.LlmError):
+        gpu.hbm_read_peak_probe(out, a, 64, 4, 256, 4, 2)
 
 
 # ---------------------------------------------------------------- temperature sampling
