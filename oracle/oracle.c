@@ -441,11 +441,10 @@ void orc_qk_norm_rope_rows(uint16_t *q, uint16_t *k, const uint16_t *v, const ui
 static float qk_dot_gpu(const uint16_t *q, const uint16_t *k, int D) {
     float acc[64];
     int lanes = D / 8;
-    for (int L = 0; L < lanes; L++) {
-        float a = 0.0f;
-        for (int e = 0; e < 8; e++) a = fmaf(bf(q[8 * L + e]), bf(k[8 * L + e]), a);
-        acc[L] = a;
-    }
+    for (int L = 0; L < lanes; L++) acc[L] = 0.0f;
+    /* each lane's chain over its 8 elements in order, the lanes side by side */
+    for (int e = 0; e < 8; e++)
+        for (int L = 0; L < lanes; L++) acc[L] = fmaf(bf(q[8 * L + e]), bf(k[8 * L + e]), acc[L]);
     return tree_sum(acc, lanes);
 }
 
@@ -520,25 +519,33 @@ static void attention_head_gpu(uint16_t *out, const uint16_t *qh, const uint16_t
     int groups = 64 / lanes;
     int per_wave = B / 4;
     int iters = per_wave / groups;
+    /* per block: wave w, position group G accumulates its positions (it = 0, 1, ...) in order
+     * for every output element d (the loop over d innermost: the same operations per element,
+     * a value row read once); then per d the groups' tree and the waves added in order */
+    float *acc = (float *)malloc((size_t)4 * groups * D * sizeof(float));
     for (int b = 0; b < nb; b++) {
+        for (int w = 0; w < 4; w++)
+            for (int G = 0; G < groups; G++) {
+                float *a = acc + ((size_t)w * groups + G) * D;
+                for (int d = 0; d < D; d++) a[d] = 0.0f;
+                for (int it = 0; it < iters; it++) {
+                    int t = b * B + w * per_wave + it * groups + G;
+                    if (t >= n) continue;
+                    const uint16_t *vt = value_cache + (size_t)t * kv_dim + kv_off;
+                    for (int d = 0; d < D; d++) a[d] = fmaf(sc[t], bf(vt[d]), a[d]);
+                }
+            }
         for (int d = 0; d < D; d++) {
             float wave_sum[4];
             for (int w = 0; w < 4; w++) {
                 float g[64];
-                for (int G = 0; G < groups; G++) {
-                    float a = 0.0f;
-                    for (int it = 0; it < iters; it++) {
-                        int t = b * B + w * per_wave + it * groups + G;
-                        if (t < n)
-                            a = fmaf(sc[t], bf(value_cache[(size_t)t * kv_dim + kv_off + d]), a);
-                    }
-                    g[G] = a;
-                }
+                for (int G = 0; G < groups; G++) g[G] = acc[((size_t)w * groups + G) * D + d];
                 wave_sum[w] = tree_sum(g, groups);
             }
             partial[(size_t)b * D + d] = ((wave_sum[0] + wave_sum[1]) + wave_sum[2]) + wave_sum[3];
         }
     }
+    free(acc);
     for (int d = 0; d < D; d++) {
         float a = partial[d];
         for (int b = 1; b < nb; b++) a = a + partial[(size_t)b * D + d];
