@@ -26,6 +26,8 @@ The JSON line also carries:
                 over rotating buffers larger than the 256 MB MALL, against 8 TB/s and against
                 the measured read peak
   cpu_baseline  the CPU oracle's decode of the same model on the host cores (bounded sample)
+  fused_layer_4B  the whole fused Qwen3-4B layer in the persistent step kernel: its mean time
+                (the kernel's own stamps) against the layer's weight bytes
   decode_configs  Qwen3-1.7B and Qwen3-4B (5-token prompt) and Qwen3-4B (8192-position N(0,1)
                 cache) greedy decode, 256 tokens each (median of 5), with bounded CPU-oracle
                 samples for 1.7B and 4B at 8192
@@ -579,6 +581,29 @@ def phase_trace(positions=range(8, 40), size="0.6B"):
     return out
 
 
+def fused_layer_rate(size, read_peak=None):
+    """The whole fused Qwen3-`size` layer inside the persistent step kernel: the mean layer time
+    of phase_trace (single-token launches at positions 8-39) against the layer's weight bytes
+    (q, k, v, o, gate, up, down and the two norms; the KV history at these positions adds under
+    0.1%)."""
+    from llm_inference_amd import model
+    c = model.qwen3_config(size)
+    H, I, QD, KVD = c.hidden_size, c.intermediate_size, c.n_heads * c.head_dim, \
+        c.n_kv_heads * c.head_dim
+    layer_bytes = 2 * (H * (QD + 2 * KVD) + QD * H + 3 * H * I + 2 * H + 2 * c.head_dim)
+    out = phase_trace(size=size)
+    gbs = layer_bytes / (out["layer_us"] * 1e-6) / 1e9
+    res = {"layer_us": out["layer_us"], "layer_bytes": layer_bytes, "GB/s": round(gbs, 1),
+           "frac_of_8TBs": round(gbs / HBM_PEAK_GBS, 4),
+           "frac_of_read_peak": round(gbs / read_peak, 4) if read_peak else None,
+           "phases_us": {k: v for k, v in out.items() if isinstance(v, dict)},
+           "method": "persistent step kernel, one token per launch at positions 8-39: mean "
+                     "layer time from the kernel's own per-layer wall-clock stamps"}
+    log(f"fused Qwen3-{size} layer in the step kernel: {out['layer_us']} us, {gbs:.1f} GB/s "
+        f"({gbs / HBM_PEAK_GBS:.1%} of 8 TB/s)")
+    return res
+
+
 def cpu_baseline(dec, prompt, budget_s=15.0):
     """The oracle's decode (fp32, the kernels' summation order) of the same model on all host
     cores: prompt positions, then greedy tokens until the time budget is spent."""
@@ -920,6 +945,7 @@ def run_bench(args):
             "qwen3_4B": decode_config("4B", 0, 256, None, read_peak),
             "qwen3_4B_ctx8192": decode_config("4B", 8192, 256, budget, read_peak),
         }
+        line["fused_layer_4B"] = fused_layer_rate("4B", read_peak)
     print(json.dumps(line), flush=True)
 
 
