@@ -804,6 +804,16 @@ __device__ __forceinline__ bool workgroup_has_rows(int R, int first_wg, int min_
     return r0 < r1;
 }
 
+// The first workgroup with q/k/v rows: the one after the attention workgroups, or with
+// S::QKV_AT_END the first of the last workgroups of the grid that hold them at S::B_QKV rows per
+// matrix wave (the host checks that these lie past the attention workgroups).
+template <class S>
+__host__ __device__ constexpr int qkv_first_wg(int grid) {
+    constexpr int rows = (S::HQ + 2 * S::HKV) * 128;
+    constexpr int per_wg = (WAVES - (S::POLLER ? 1 : 0)) * S::B_QKV;
+    return S::QKV_AT_END ? grid - (rows + per_wg - 1) / per_wg : S::HQ;
+}
+
 // When a matrix workgroup requests the down rows (PF_D) and the next layer's q/k/v rows
 // (PF_QKV). Loads complete in order, so a request placed before a poll holds the poll until it
 // lands, and weights streaming during a handoff slow it: at 0.6B both go out while attention
@@ -860,12 +870,14 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
     int q0, q1, o0, o1, g0, g1;
     constexpr int FW = S::POLLER ? 1 : 0;  // first wave with matrix rows
     constexpr bool OW = S::POLLER;         // staging by wave 0 alone
-    // a wave takes at least one prefetched batch of q/k/v rows: at 0.6B 4 rows on 1024 waves
-    // instead of 3 on 1366 (+0.8%; more o, gate/up or q/k/v rows per wave measured 3-15% slower)
-    phase_rows<FW>(QD + 2 * KVD, S::HQ, q0, q1, S::B_QKV);
+    // a wave takes at least one prefetched batch of q/k/v rows (at 0.6B 4 rows on 1024 waves
+    // instead of 3 on 1366: +0.8%), placed after the attention workgroups or, with
+    // S::QKV_AT_END, on the last workgroups of the grid
+    const int q_first = qkv_first_wg<S>((int)gridDim.x);
+    phase_rows<FW>(QD + 2 * KVD, q_first, q0, q1, S::B_QKV);
     phase_rows<FW>(H, S::HQ, o0, o1);
     phase_rows<FW>(I, S::HQ, g0, g1);
-    const bool wg_q = workgroup_has_rows<FW>(QD + 2 * KVD, S::HQ, S::B_QKV);
+    const bool wg_q = workgroup_has_rows<FW>(QD + 2 * KVD, q_first, S::B_QKV);
     const bool wg_o = workgroup_has_rows<FW>(H, S::HQ);
     const bool wg_g = workgroup_has_rows<FW>(I, S::HQ);
 
@@ -1209,7 +1221,18 @@ struct Shape {
     // kernel 424 + 0.53 us per position at 0.6B, 892 + 0.52 at 1.7B, 1730 + 0.72 at 4B; hipGraph
     // 783 + 0.024, 1120 + 0.016, 2032 + 0.02 (us per token)
     static constexpr int SWITCH_POS = H <= 1024 ? 736 : H <= 2048 ? 480 : 448;
-    static constexpr int B_QKV = H <= 1024 ? 4 : 2;  // 4B: 575.4-575.9 tokens/s, 1 row 544.7
+    // q/k/v rows per wave (one prefetched batch; 4B: 575.4-575.9 tokens/s, 1 row 544.7) and
+    // where they go. A CU's vector-memory requests complete in order, so a workgroup's poll
+    // lands only after every weight request it made before the poll. At 0.6B every matrix
+    // workgroup requests its o, gate/up and down rows and the next layer's q/k/v rows while
+    // attention runs; the o rows' workgroups (16-143) also held q/k/v rows, 208 KB in all, and
+    // their poll of the attention output landed 0.9-2.1 us after the output existed. With the
+    // q/k/v rows on the last 64 workgroups (8 per wave), which own no o/down rows, that spread
+    // is 0.2 us and the layer ~1 us shorter, less 0.3 us for the longer q/k/v GEMV: 2300-2323
+    // against 2282-2292 tokens/s (alternating runs on four boxes). Spreading the o/down or
+    // gate/up rows over more workgroups instead measured 1-3.5% slower (more pollers per copy).
+    static constexpr int B_QKV = H == 1024 ? 8 : H < 1024 ? 4 : 2;
+    static constexpr bool QKV_AT_END = H == 1024;
     static constexpr int B_O = H <= 1024 ? 1 : (HQ * 128 <= 2048 ? 2 : 1);
     static constexpr int B_GU = H <= 1024 ? 2 : 1;
     static constexpr int B_DOWN = 1;
@@ -1262,6 +1285,11 @@ static const void *step_kernel_for(const Config *c) {
 // at most 64 residual rows per matrix wave (7 matrix waves per workgroup when wave 0 polls).
 static bool step_grid_fits(const Config *c, int grid) {
     if (grid <= 0 || grid > 1024 || grid < 2 * c->n_heads) return false;
+#define QKV_FITS(S)                                                                         \
+    if (step_kernel_for(c) == (const void *)step_kernel<S> && qkv_first_wg<S>(grid) < S::HQ)   \
+        return false;
+    QKV_FITS(Qwen3_06B) QKV_FITS(Qwen3_17B) QKV_FITS(Qwen3_4B) QKV_FITS(SmallTest)
+#undef QKV_FITS
     // a wave keeps its residual rows of x in one register (lane j: its row j)
     return rows_per_wave(c->hidden_size, (grid - c->n_heads) * WAVES) <= 64;
 }
