@@ -172,8 +172,7 @@ void hbm_read_peak_probe(unsigned *out, const void *a, size_t n_bytes, int block
 /* No counterpart in the reference. Decode attention as attention_forward computes it, without
  * the `att` argument, for callers that cannot allocate device memory (code under stream
  * capture, tight serving loops, harnesses that forbid hipMalloc). It allocates nothing: its
- * workspace is a
- * library-owned device array of 2^20 floats (4 MiB) per device, so
+ * workspace is a library-owned device array of 2^20 floats (4 MiB) per device, so
  * attention_workspace_floats(n_heads, head_dim, max_seq) must not exceed 1048576 (Qwen3-4B's 32
  * heads of 128 fit up to 10798 positions); larger sizes are an error and nothing is launched.
  * Every call on a device shares that device's array: calls that overlap on one device race. */
