@@ -401,17 +401,17 @@ def traffic_from_profiles(tokens):
     return round(float(m.group(1)) * tokens) if m else None
 
 
-def pmc_workload(steps):
-    """The bench's timed launch alone, for counter collection (rocprofv3 --pmc): the 5-token
-    prompt (one launch per position), then `steps` greedy tokens in one launch of the persistent
-    step kernel, then four 256 MiB device-to-device copies whose FETCH_SIZE and WRITE_SIZE
-    calibrate the counters (known bytes)."""
+def pmc_workload(steps, size="0.6B"):
+    """The bench's timed launch alone, for counter collection (rocprofv3 --pmc): Qwen3-`size`
+    (default 0.6B, the bench step), the 5-token prompt (one launch per position), then `steps`
+    greedy tokens in one launch of the persistent step kernel, then four 256 MiB device-to-device
+    copies whose FETCH_SIZE and WRITE_SIZE calibrate the counters (known bytes)."""
     import numpy as np
     import torch
     pkg = load_package()
     from llm_inference_amd import model
     pkg.lib()
-    cfg = model.qwen3_config("0.6B", max_seq_len=5 + steps + 8)
+    cfg = model.qwen3_config(size, max_seq_len=5 + steps + 8)
     dec = model.Decoder(cfg, ("synth", 0, 0.02, 0.1))
     dec.capture_graph()
     prompt = [int(t) for t in np.random.default_rng(0).integers(0, cfg.vocab_size, 5)]
@@ -763,8 +763,9 @@ def main():
                          "object of a program counter a profiler reports after the run)")
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the Qwen3-1.7B and Qwen3-4B (8192-position cache) decode lines")
-    ap.add_argument("--pmc-workload", action="store_true",
-                    help="only run the short counter-collection workload")
+    ap.add_argument("--pmc-workload", nargs="?", const="0.6B", choices=["0.6B", "1.7B", "4B"],
+                    help="only run the short counter-collection workload (one 256-token launch "
+                         "of the step kernel; default size 0.6B)")
     ap.add_argument("--gemv-workload", action="store_true",
                     help="only launch the Qwen3-4B GEMVs at 1/8, 1/4, 1/2 and all of their rows "
                          "(for a rocprofv3 launch-cost fit and byte counters)")
@@ -784,7 +785,7 @@ def main():
         sys.exit(2)
 
     if args.pmc_workload:
-        pmc_workload(GEN_TOKENS)
+        pmc_workload(GEN_TOKENS, args.pmc_workload)
     elif args.gemv_workload:
         gemv_workload()
     elif args.config4_workload:
