@@ -805,12 +805,13 @@ __device__ __forceinline__ bool workgroup_has_rows(int R, int first_wg, int min_
 }
 
 // The first workgroup with q/k/v rows: the one after the attention workgroups, or with
-// S::QKV_AT_END the first of the last workgroups of the grid that hold them at S::B_QKV rows per
-// matrix wave (the host checks that these lie past the attention workgroups).
+// S::QKV_AT_END the first of the last workgroups of the grid that hold them at
+// S::QKV_PER_WAVE rows per matrix wave (the host checks that these lie past the attention
+// workgroups).
 template <class S>
 __host__ __device__ constexpr int qkv_first_wg(int grid) {
     constexpr int rows = (S::HQ + 2 * S::HKV) * 128;
-    constexpr int per_wg = (WAVES - (S::POLLER ? 1 : 0)) * S::B_QKV;
+    constexpr int per_wg = (WAVES - (S::POLLER ? 1 : 0)) * S::QKV_PER_WAVE;
     return S::QKV_AT_END ? grid - (rows + per_wg - 1) / per_wg : S::HQ;
 }
 
@@ -874,10 +875,11 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
     // instead of 3 on 1366: +0.8%), placed after the attention workgroups or, with
     // S::QKV_AT_END, on the last workgroups of the grid
     const int q_first = qkv_first_wg<S>((int)gridDim.x);
-    phase_rows<FW>(QD + 2 * KVD, q_first, q0, q1, S::B_QKV);
+    constexpr int Q_MIN = S::QKV_AT_END ? 1 : S::B_QKV;  // rows per wave at least
+    phase_rows<FW>(QD + 2 * KVD, q_first, q0, q1, Q_MIN);
     phase_rows<FW>(H, S::HQ, o0, o1);
     phase_rows<FW>(I, S::HQ, g0, g1);
-    const bool wg_q = workgroup_has_rows<FW>(QD + 2 * KVD, q_first, S::B_QKV);
+    const bool wg_q = workgroup_has_rows<FW>(QD + 2 * KVD, q_first, Q_MIN);
     const bool wg_o = workgroup_has_rows<FW>(H, S::HQ);
     const bool wg_g = workgroup_has_rows<FW>(I, S::HQ);
 
@@ -1227,12 +1229,16 @@ struct Shape {
     // workgroup requests its o, gate/up and down rows and the next layer's q/k/v rows while
     // attention runs; the o rows' workgroups (16-143) also held q/k/v rows, 208 KB in all, and
     // their poll of the attention output landed 0.9-2.1 us after the output existed. With the
-    // q/k/v rows on the last 64 workgroups (8 per wave), which own no o/down rows, that spread
-    // is 0.2 us and the layer ~1 us shorter, less 0.3 us for the longer q/k/v GEMV: 2300-2323
-    // against 2282-2292 tokens/s (alternating runs on four boxes). Spreading the o/down or
-    // gate/up rows over more workgroups instead measured 1-3.5% slower (more pollers per copy).
+    // q/k/v rows on the last workgroups, which own no o/down rows, that spread is 0.2 us and
+    // the layer ~1 us shorter, less 0.3 us for the longer q/k/v GEMV. 8 rows per wave on the
+    // last 64: 2300-2323 against 2282-2292 tokens/s (alternating runs on four boxes); 6 per
+    // wave (one batch of 8 with two empty rows) on the last 86, so that the 38 of them that also
+    // own gate/up rows request 160 KB instead of 192 KB before their gate/up poll: 2316-2333
+    // against 2294-2313 (two boxes; 5 per wave +0.2%, 7 +0.5%). Spreading the o/down or gate/up
+    // rows over more workgroups instead measured 1-3.5% slower (more pollers per copy).
     static constexpr int B_QKV = H == 1024 ? 8 : H < 1024 ? 4 : 2;
     static constexpr bool QKV_AT_END = H == 1024;
+    static constexpr int QKV_PER_WAVE = H == 1024 ? 6 : B_QKV;
     static constexpr int B_O = H <= 1024 ? 1 : (HQ * 128 <= 2048 ? 2 : 1);
     static constexpr int B_GU = H <= 1024 ? 2 : 1;
     static constexpr int B_DOWN = 1;
