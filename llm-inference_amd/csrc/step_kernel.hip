@@ -1245,10 +1245,11 @@ struct Shape {
     // 0.6B: 4 rows +0.4% over 8, 16 spills; 4B: 4 rows spill (156 bytes), 561.1 against 575.4
     static constexpr int B_LM = H <= 2048 ? 4 : 2;
     // copies of x, the attention output and the SwiGLU output (at most STEP_REPLICAS), each
-    // 1 KB off the 4 KB grid (step_replica_stride): 4 at every shape (0.6B: 2291-2294 tokens/s
-    // against 2280-2282 with 8, on two boxes, and 2301 against 2221 with 2 and 2067 with 3 on a
-    // third; 1.7B: 1115 against 1074 with 8)
-    static constexpr int REPLICAS = 4;
+    // 1 KB off the 4 KB grid (step_replica_stride). 0.6B: 8 with the q/k/v rows at the end of the
+    // grid (2339-2342 tokens/s against 2332-2335 with 4, five alternating rounds on two boxes;
+    // 2 copies 2258); before that layout 4 measured faster (2291-2294 against 2280-2282 with 8,
+    // 2301 against 2221 with 2 and 2067 with 3). 1.7B and 4B: 4 (1.7B 1115 against 1074 with 8).
+    static constexpr int REPLICAS = H == 1024 ? 8 : 4;
     // 1.7B: the down rows with attention 1050 -> 1075 tokens/s, the q/k/v rows too 1005; 4B
     // (5-token prompt): 575.8-576.4 as below, the q/k/v rows after the gate/up poll 572.6-572.8,
     // the down rows after the o poll 466.2-466.3
