@@ -96,7 +96,9 @@ def device_peak(pkg, stream):
     then a 4 GiB read (hbm_read_peak_probe), median of 20 after 3 warm-ups per launch shape,
     the best of 4 workgroup sizes x 4 workgroups-per-CU counts x 3 loads-in-flight counts x 2
     layouts (grid-stride; one range per workgroup, keys ending in c). The read is 4 GiB so that
-    a launch's fixed cost (a few microseconds) is under 1% of its ~0.6 ms."""
+    a launch's fixed cost (a few microseconds) is under 1% of its ~0.6 ms. Then the copy peak:
+    1 GiB copied by hbm_copy_peak_probe, median of 20 after 3 warm-ups per launch shape, the
+    best of 4 workgroup counts x 2 workgroup sizes x 3 chunks-in-flight counts."""
     import torch
     L = pkg.lib()
     ts = torch.cuda.ExternalStream(stream)
@@ -140,19 +142,41 @@ def device_peak(pkg, stream):
     best = max(shapes, key=shapes.get)
     torch.cuda.synchronize()
     del src
+    src = torch.empty(copy_bytes // 2, dtype=torch.int16, device="cuda")
+    L.synth_fill(src.data_ptr(), src.numel(), 321, 0, 0.0, 1.0, stream)
+    dst = torch.empty_like(src)
+    copy_shapes = {}
+    for chunks in (2, 4, 8):
+        for threads in (256, 512):
+            for per_cu in (1, 2, 4, 8):
+                blocks = per_cu * cus
+                ms = median_ms(lambda: pkg.hbm_copy_peak_probe(dst, src, copy_bytes, blocks,
+                                                                threads, chunks, stream=stream),
+                               3, 20)
+                copy_shapes[f"{blocks}x{threads}x{chunks}"] = round(
+                    2 * copy_bytes / (ms * 1e-3) / 1e9, 1)
+    cbest = max(copy_shapes, key=copy_shapes.get)
+    torch.cuda.synchronize()
+    del src, dst
     res = {"copy_GB/s": round(copy_gbs, 1), "read_GB/s": shapes[best], "read_best_shape": best,
+           "copy_peak_GB/s": copy_shapes[cbest], "copy_peak_shape": cbest,
+           "copy_peak_shapes_GB/s": copy_shapes,
            "read_shapes_GB/s": shapes, "copy_bytes": copy_bytes, "read_bytes": read_bytes,
            "method": "bench/bandwidth.cu: 1 GiB D2D copy (2x bytes), median of 20 after 200 "
                      "warm-ups; 4 GiB read, median of 20, best of 96 launch shapes "
                      "(workgroups x threads x 16-byte loads in flight per thread, grid-stride "
-                     "or a range per workgroup: c)"}
-    log(f"device peak: copy {res['copy_GB/s']} GB/s, read {res['read_GB/s']} GB/s ({best})")
+                     "or a range per workgroup: c); copy peak: 1 GiB, 2x the bytes, median of "
+                     "20, best of 24 launch shapes (workgroups x threads x 16-byte chunks in "
+                     "flight per thread)"}
+    log(f"device peak: copy {res['copy_GB/s']} GB/s (copy_), copy peak {copy_shapes[cbest]} GB/s "
+        f"({cbest}), read {res['read_GB/s']} GB/s ({best})")
     return res
 
 
-def fused_kernel_table(pkg, stream, read_peak_gbs):
+def fused_kernel_table(pkg, stream, read_peak_gbs, copy_peak_gbs=None):
     """GB/s of the fused kernels at Qwen3-4B widths and the sweep sizes (algorithmic bytes),
-    against 8 TB/s and against the measured read peak."""
+    against 8 TB/s and against the measured read peak; the many-row sweeps, whose traffic is a
+    third to a half writes, also against the measured copy peak."""
     import torch
     from llm_inference_amd import model
     L = pkg.lib()
@@ -164,13 +188,17 @@ def fused_kernel_table(pkg, stream, read_peak_gbs):
         L.synth_fill(t.data_ptr(), n, 123, sid, mean, std, stream)
         return t
 
-    def row(name, nbytes, seconds, shape):
+    def row(name, nbytes, seconds, shape, vs_copy=False):
         gbs = nbytes / seconds / 1e9
         out[name] = {"shape": shape, "bytes": nbytes, "us": round(seconds * 1e6, 3),
                      "GB/s": round(gbs, 1), "frac_of_8TBs": round(gbs / HBM_PEAK_GBS, 4),
                      "frac_of_read_peak": round(gbs / read_peak_gbs, 4) if read_peak_gbs else None}
+        if vs_copy and copy_peak_gbs:
+            out[name]["frac_of_copy_peak"] = round(gbs / copy_peak_gbs, 4)
         log(f"  {name:28s} {seconds * 1e6:9.2f} us {gbs:8.1f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of "
-            f"8 TB/s" + (f", {gbs / read_peak_gbs:.1%} of the read peak)" if read_peak_gbs else ")"))
+            f"8 TB/s" + (f", {gbs / read_peak_gbs:.1%} of the read peak" if read_peak_gbs else "")
+            + (f", {gbs / copy_peak_gbs:.1%} of the copy peak" if vs_copy and copy_peak_gbs
+               else "") + ")")
 
     H, I, qd, kvd, hq, hkv, D = 2560, 9728, 4096, 1024, 32, 8, 128
     # gate_up 4B: 2*I*H*2 weights + x + act
@@ -214,7 +242,7 @@ def fused_kernel_table(pkg, stream, read_peak_gbs):
     g = fill(H, 1.0, 0.1)
     f = lambda i: pkg.rmsnorm_forward(ys[i % k], xs[i % k], g, R, H, 1e-6, stream=stream)
     f(0)
-    row("rmsnorm 4096x2560", nb, timer.time(f, 4 * k), [R, H])
+    row("rmsnorm 4096x2560", nb, timer.time(f, 4 * k), [R, H], vs_copy=True)
     del xs, ys
     # qk_norm_rope sweep: 4096 tokens x (32 q + 8 kv) heads, positions 0..4095
     T = 4096
@@ -230,7 +258,7 @@ def fused_kernel_table(pkg, stream, read_peak_gbs):
     f = lambda i: pkg.qk_norm_rope_rows(qs[i % k], ks[i % k], vs[i % k], qn, kn, kcs[i % k],
                                         vcs[i % k], posd, T, hq, hkv, D, 1e-6, 1e6, stream=stream)
     f(0)
-    row("qk_norm_rope 4096x(32+8)x128", nb, timer.time(f, 4 * k), [T, hq + hkv, D])
+    row("qk_norm_rope 4096x(32+8)x128", nb, timer.time(f, 4 * k), [T, hq + hkv, D], vs_copy=True)
     del qs, ks, vs, kcs, vcs
     # SwiGLU sweep 4096 x 9728
     n = 4096 * I
@@ -241,7 +269,7 @@ def fused_kernel_table(pkg, stream, read_peak_gbs):
     acts = [fill(n) for _ in range(k)]
     f = lambda i: pkg.swiglu_forward(acts[i % k], gs[i % k], us[i % k], n, stream=stream)
     f(0)
-    row("swiglu 4096x9728", nb, timer.time(f, 4 * k), [4096, I])
+    row("swiglu 4096x9728", nb, timer.time(f, 4 * k), [4096, I], vs_copy=True)
     del gs, us, acts
 
     # config 1: the Qwen3-0.6B layer's kernels at decode (one token; algorithmic bytes as in
@@ -888,7 +916,9 @@ def run_bench(args):
     log(f"step kernel: {launch_bytes / 1e6:.1f} MB per launch, {achieved:.1f} GB/s")
     traffic = traffic_from_profiles(n_gen) if launches == 1 else None
 
-    table = None if args.no_kernel_table else fused_kernel_table(pkg, dec.stream, read_peak)
+    copy_peak = peak["copy_peak_GB/s"] if peak else None
+    table = None if args.no_kernel_table else fused_kernel_table(pkg, dec.stream, read_peak,
+                                                                 copy_peak)
     if table and not args.no_cpu_baseline:
         cpu_kernel_rates(table)
     cpu = None if args.no_cpu_baseline else cpu_baseline(dec, prompt)

@@ -169,6 +169,14 @@ void hbm_stream_probe(void *dst, const void *a, const void *b, size_t n_bytes, i
 void hbm_read_peak_probe(unsigned *out, const void *a, size_t n_bytes, int blocks, int threads,
                          int loads_in_flight, int contiguous, hipStream_t stream);
 
+/* Measurement helper: the device copy peak (the reference's bench/bandwidth.cu:25-116 measures a
+ * device-to-device copy beside its read kernel). Copies n_bytes of a to dst (n_bytes % 16 == 0,
+ * both 16-byte aligned, not overlapping) grid-stride with `blocks` workgroups of `threads`
+ * threads (64..1024, a power of two), each thread requesting chunks_in_flight (1, 2, 4 or 8)
+ * non-temporal 16-byte loads before it stores them. */
+void hbm_copy_peak_probe(void *dst, const void *a, size_t n_bytes, int blocks, int threads,
+                         int chunks_in_flight, hipStream_t stream);
+
 /* No counterpart in the reference. Decode attention as attention_forward computes it, without
  * the `att` argument, for callers that cannot allocate device memory (code under stream
  * capture, tight serving loops, harnesses that forbid hipMalloc). It allocates nothing: its

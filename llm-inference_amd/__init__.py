@@ -21,7 +21,7 @@ __all__ = [
     "gemv_residual_forward", "qkv_forward", "gate_up_forward", "qk_norm_rope_forward",
     "qk_norm_rope_rows", "attention_forward", "argmax_forward", "swiglu_forward",
     "attention_workspace_floats", "rmsnorm_qkv_forward", "rmsnorm_gemv_forward",
-    "rmsnorm_gate_up_forward", "hbm_stream_probe", "hbm_read_peak_probe", "sample_forward",
+    "rmsnorm_gate_up_forward", "hbm_stream_probe", "hbm_read_peak_probe", "hbm_copy_peak_probe", "sample_forward",
     "qk_norm_rope_attention_forward", "dump_open",
     "dump_close", "dump_enabled", "attention_forward_noalloc", "EXPORTED_SYMBOLS",
     "qk_norm_rope_attention_one_pass", "attention_one_pass_bytes", "attention_one_pass_supported",
@@ -33,7 +33,7 @@ EXPORTED_SYMBOLS = [
     "qkv_forward", "gate_up_forward", "qk_norm_rope_forward", "attention_forward",
     "argmax_forward", "qk_norm_rope_rows", "swiglu_forward", "attention_workspace_floats",
     "rmsnorm_qkv_forward", "rmsnorm_gemv_forward", "rmsnorm_gate_up_forward",
-    "hbm_stream_probe", "hbm_read_peak_probe", "sample_forward", "sample_temperature",
+    "hbm_stream_probe", "hbm_read_peak_probe", "hbm_copy_peak_probe", "sample_forward", "sample_temperature",
     "dump_open", "dump_close",
     "dump_enabled", "dump_bf16", "dump_f32", "llm_set_exit_on_error", "llm_last_error", "llm_clear_error",
     "load_config", "load_weights", "free_weights", "print_weight_checksums",
@@ -75,6 +75,7 @@ _SIGS = {
     "rmsnorm_gate_up_forward": (None, [_vp] * 5 + [_f, _i, _i, _vp]),
     "hbm_stream_probe": (None, [_vp, _vp, _vp, _sz, _i, _vp]),
     "hbm_read_peak_probe": (None, [_vp, _vp, _sz, _i, _i, _i, _i, _vp]),
+    "hbm_copy_peak_probe": (None, [_vp, _vp, _sz, _i, _i, _i, _vp]),
     "qk_norm_rope_attention_forward": (None, [_vp] * 9 + [_vp, _i, _i, _i, _f, _f, _i, _f, _vp]),
     "qk_norm_rope_attention_one_pass": (None, [_vp] * 11 + [_i, _i, _i, _f, _f, _i, _f, _vp]),
     "attention_one_pass_bytes": (_sz, [_i, _i, _i]),
@@ -303,6 +304,18 @@ def hbm_read_peak_probe(out, a, n_bytes, blocks, threads, loads_in_flight=4, con
     equals 0x9e3779b9."""
     _call(lib().hbm_read_peak_probe, _ptr(out), _ptr(a), n_bytes, blocks, threads,
           loads_in_flight, contiguous, _stream(stream))
+
+
+def hbm_copy_peak_probe(dst, a, n_bytes, blocks, threads, chunks_in_flight=4, stream=None):
+    """Copies n_bytes of `a` to `dst` grid-stride with `blocks` workgroups of `threads` threads,
+    each thread requesting chunks_in_flight 16-byte loads before it stores them (the copy-peak
+    probe)."""
+    for name, t in (("dst", dst), ("a", a)):
+        if not isinstance(t, int) and t.numel() * t.element_size() < n_bytes:
+            raise LlmError(f"{name} holds {t.numel() * t.element_size()} bytes, the probe copies "
+                           f"{n_bytes}")
+    _call(lib().hbm_copy_peak_probe, _ptr(dst), _ptr(a), n_bytes, blocks, threads,
+          chunks_in_flight, _stream(stream))
 
 
 def sample_forward(out, x, n, inv_temp, u, stream=None):

@@ -2527,6 +2527,50 @@ extern "C" void hbm_read_peak_probe(unsigned *out, const void *a, size_t n_bytes
     LAUNCH_OK();
 }
 
+// The device copy peak: a grid-stride copy, each thread requesting U non-temporal 16-byte loads
+// (chunks blockDim apart) before it stores them. Every chunk index is checked against n16.
+template <int U>
+__global__ __launch_bounds__(1024) void copy_peak_kernel(u32x4 *__restrict__ d,
+                                                         const u32x4 *__restrict__ a, size_t n16) {
+    const size_t tile = (size_t)blockDim.x * U, stride = (size_t)gridDim.x * tile;
+    for (size_t base = (size_t)blockIdx.x * tile + threadIdx.x; base < n16; base += stride) {
+        u32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const size_t i = base + (size_t)u * blockDim.x;
+            v[u] = i < n16 ? __builtin_nontemporal_load(a + i) : u32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const size_t i = base + (size_t)u * blockDim.x;
+            if (i < n16) __builtin_nontemporal_store(v[u], d + i);
+        }
+    }
+}
+
+extern "C" void hbm_copy_peak_probe(void *dst, const void *a, size_t n_bytes, int blocks,
+                                    int threads, int chunks_in_flight, hipStream_t stream) {
+    if (n_bytes % 16 != 0 || !aligned16(a) || !aligned16(dst) || blocks < 1 ||
+        blocks > (1 << 20) || (threads != 64 && threads != 128 && threads != 256 &&
+                               threads != 512 && threads != 1024) ||
+        (chunks_in_flight != 1 && chunks_in_flight != 2 && chunks_in_flight != 4 &&
+         chunks_in_flight != 8)) {
+        llm_fail("hbm_copy_peak_probe: %zu bytes (a multiple of 16, 16-byte aligned), %d blocks "
+                 "of %d threads (64..1024, a power of two), %d chunks in flight (1, 2, 4 or 8)",
+                 n_bytes, blocks, threads, chunks_in_flight);
+        return;
+    }
+    if (n_bytes == 0) return;
+    u32x4 *d = (u32x4 *)dst;
+    const u32x4 *p = (const u32x4 *)a;
+    const size_t n16 = n_bytes / 16;
+    if (chunks_in_flight == 1) copy_peak_kernel<1><<<blocks, threads, 0, stream>>>(d, p, n16);
+    else if (chunks_in_flight == 2) copy_peak_kernel<2><<<blocks, threads, 0, stream>>>(d, p, n16);
+    else if (chunks_in_flight == 4) copy_peak_kernel<4><<<blocks, threads, 0, stream>>>(d, p, n16);
+    else copy_peak_kernel<8><<<blocks, threads, 0, stream>>>(d, p, n16);
+    LAUNCH_OK();
+}
+
 // ------------------------------------------------------------------------------------------
 // argmax (src/kernels.cu:499-544), two stages
 // ------------------------------------------------------------------------------------------

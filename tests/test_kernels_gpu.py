@@ -621,6 +621,30 @@ def test_hbm_read_peak_probe(gpu):
         gpu.hbm_read_peak_probe(out, a, 64, 4, 256, 4, 2)
 
 
+def test_hbm_copy_peak_probe(gpu):
+    """The copy-peak probe copies every chunk exactly once and nothing past n_bytes: random words
+    into a destination filled with a sentinel one chunk longer, for every chunks-in-flight count,
+    with lengths that are not multiples of the grid's tile; bad launch shapes are refused."""
+    import torch
+    ident("hbm_copy_peak_probe")
+    g = torch.Generator(device="cpu").manual_seed(11)
+    for U in (1, 2, 4, 8):
+        for blocks, threads in [(3, 256), (2, 1024), (7, 64)]:
+            n16 = U * blocks * threads * 3 + 5
+            a = torch.randint(-2**31, 2**31 - 1, (n16 * 4,), generator=g, dtype=torch.int32).cuda()
+            d = torch.full((n16 * 4 + 4,), 0x5a5a5a5a, dtype=torch.int32, device="cuda")
+            gpu.hbm_copy_peak_probe(d, a, n16 * 16, blocks, threads, U)
+            torch.cuda.synchronize()
+            assert torch.equal(d[:n16 * 4], a), (U, blocks, threads)
+            assert torch.all(d[n16 * 4:] == 0x5a5a5a5a), (U, blocks, threads)
+    with pytest.raises(gpu.LlmError):
+        gpu.hbm_copy_peak_probe(d, a, 64, 4, 100)
+    with pytest.raises(gpu.LlmError):
+        gpu.hbm_copy_peak_probe(d, a, 24, 4, 256)
+    with pytest.raises(gpu.LlmError):
+        gpu.hbm_copy_peak_probe(d, a, 64, 4, 256, 3)
+
+
 # ---------------------------------------------------------------- temperature sampling
 
 def test_sample_forward(gpu, oracle):
