@@ -150,7 +150,7 @@ enum { ATTN_AUTO = 0, ATTN_SEPARATE = 1, ATTN_IN_SCORES = 2, ATTN_ONE_PASS = 3 }
  * generate_greedy runs its tokens in one launch) for the positions below
  * RunState::step_switch_pos, and a hipGraph of the per-layer kernels from there on: the kernel's
  * attention runs one workgroup per query head, so its cost grows with the history faster than
- * the graph's (crossover 736 / 480 / 448 positions at 0.6B / 1.7B / 4B; 5-token prompt: 2356 /
+ * the graph's (crossover 736 / 512 / 480 positions at 0.6B / 1.7B / 4B; 5-token prompt: 2356 /
  * 1121 / 578 tokens/s against 1278 / 893 / 492). Other shapes: the hipGraph. STEP_GRAPH:
  * always the hipGraph. STEP_PERSISTENT: the persistent kernel at every position (max_seq at
  * most 8192) or an error. */

@@ -1221,8 +1221,10 @@ struct Shape {
     // STEP_AUTO's switch to the hipGraph step: the crossover of the two steps' per-token time,
     // measured on MI355X (64 greedy tokens after an N(0, 1) cache of 5..8100 positions): step
     // kernel 424 + 0.53 us per position at 0.6B, 892 + 0.52 at 1.7B, 1730 + 0.72 at 4B; hipGraph
-    // 783 + 0.024, 1120 + 0.016, 2032 + 0.02 (us per token)
-    static constexpr int SWITCH_POS = H <= 1024 ? 736 : H <= 2048 ? 480 : 448;
+    // 783 + 0.024, 1120 + 0.016, 2032 + 0.02 (us per token). Measured again around the switch
+    // (kernel / graph tokens/s): 0.6B 704 1334 / 1270, 768 1226 / 1269; 1.7B 480 919 / 899, 544
+    // 879 / 896; 4B 448 516 / 499, 512 486 / 500.
+    static constexpr int SWITCH_POS = H <= 1024 ? 736 : H <= 2048 ? 512 : 480;
     // q/k/v rows per wave (one prefetched batch; 4B: 575.4-575.9 tokens/s, 1 row 544.7) and
     // where they go. A CU's vector-memory requests complete in order, so a workgroup's poll
     // lands only after every weight request it made before the poll. At 0.6B every matrix

@@ -705,27 +705,32 @@ def test_persistent_step_long_context(qwen06b, oracle):
 def test_persistent_step_wide_shapes_long_history(gpu, oracle, size):
     """The 1.7B and 4B specialisations of the persistent step (2 and 4 query heads per kv head)
     where the bench and STEP_AUTO run them: single positions 260 (five 64-position blocks) and
-    447 (seven; the last 4B position before the switch to the hipGraph) after a KV cache filled
-    with N(0, 1) below them, at full widths with 2 layers. Logits, argmax and the KV rows written
-    bit-identical to the oracle; then an 8-token generate from 440 in one launch."""
-    ident(f"persistent step {size} widths at positions 260 and 447")
+    the last position before STEP_AUTO's switch to the hipGraph (511 at 1.7B, 479 at 4B: eight
+    blocks) after a KV cache filled with N(0, 1) below them, at full widths with 2 layers.
+    Logits, argmax and the KV rows written bit-identical to the oracle; then an 8-token generate
+    that ends at that position, in one launch."""
+    last = {"1.7B": 511, "4B": 479}[size]
+    ident(f"persistent step {size} widths at positions 260 and {last}")
     from llm_inference_amd import model
-    cfg = model.qwen3_config(size, n_layers=2, max_seq_len=512)
+    S = 528
+    cfg = model.qwen3_config(size, n_layers=2, max_seq_len=S)
     dec = model.Decoder(cfg, ("synth", 31, 0.02, 0.1))
     try:
         rng = np.random.default_rng(447)
         kvd = cfg.n_kv_heads * cfg.head_dim
-        k = rand_bf16(rng, (cfg.n_layers, 512, kvd))
-        v = rand_bf16(rng, (cfg.n_layers, 512, kvd))
+        k = rand_bf16(rng, (cfg.n_layers, S, kvd))
+        v = rand_bf16(rng, (cfg.n_layers, S, kvd))
         dec.set_kv_cache(k, v)
         w = dec.host_weights()
-        orc = oracle.Model(oracle_cfg(cfg), w, max_seq=512)
+        orc = oracle.Model(oracle_cfg(cfg), w, max_seq=S)
         del w
         orc.bufs["key_cache"][:] = k.reshape(-1)
         orc.bufs["value_cache"][:] = v.reshape(-1)
+        dec.capture_graph("auto")
+        assert dec.s.step_switch_pos == last + 1
         dec.capture_graph("persistent")
         assert dec.persistent
-        for pos in (260, 447):
+        for pos in (260, last):
             tok = int(rng.integers(0, cfg.vocab_size))
             dec.forward(tok, pos)
             nxt = dec.sample_argmax()
@@ -737,10 +742,10 @@ def test_persistent_step_wide_shapes_long_history(gpu, oracle, size):
             ov = orc.bufs["value_cache"].reshape(v.shape)
             assert np.array_equal(kk[:, pos], ok[:, pos]), pos
             assert np.array_equal(vv[:, pos], ov[:, pos]), pos
-        got = dec.generate_greedy(nxt, 440, 8)
+        got = dec.generate_greedy(nxt, last - 7, 8)
         t, want = nxt, []
         for i in range(8):
-            t = orc.forward(t, 440 + i, oracle.GPU_ORDER)
+            t = orc.forward(t, last - 7 + i, oracle.GPU_ORDER)
             want.append(t)
         assert got == want
     finally:
