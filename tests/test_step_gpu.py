@@ -701,6 +701,56 @@ def test_persistent_step_long_context(qwen06b, oracle):
         dec.close()
 
 
+def test_persistent_step_4b_longest_history(gpu, oracle):
+    """The 4B specialisation of the persistent step (four query heads per kv head) at the longest
+    history it holds (8192 positions of scores per head in LDS): one position at 8183, then an
+    8-token generate in one launch ending at 8191, after a KV cache filled with N(0, 1) below,
+    full widths with 2 layers. Logits, argmax, the KV rows written and the generated tokens
+    bit-identical to the oracle; the next position is refused."""
+    ident("persistent step 4B widths at positions 8183..8191")
+    from llm_inference_amd import LlmError, model
+    S = 8192
+    cfg = model.qwen3_config("4B", n_layers=2, max_seq_len=S)
+    dec = model.Decoder(cfg, ("synth", 37, 0.02, 0.1))
+    try:
+        rng = np.random.default_rng(8183)
+        kvd = cfg.n_kv_heads * cfg.head_dim
+        k = rand_bf16(rng, (cfg.n_layers, S, kvd))
+        v = rand_bf16(rng, (cfg.n_layers, S, kvd))
+        dec.set_kv_cache(k, v)
+        w = dec.host_weights()
+        orc = oracle.Model(oracle_cfg(cfg), w, max_seq=S)
+        del w
+        orc.bufs["key_cache"][:] = k.reshape(-1)
+        orc.bufs["value_cache"][:] = v.reshape(-1)
+        dec.capture_graph("persistent")
+        assert dec.persistent
+        tok = int(rng.integers(0, cfg.vocab_size))
+        dec.forward(tok, 8183)
+        nxt = dec.sample_argmax()
+        ref = orc.forward(tok, 8183, oracle.GPU_ORDER)
+        assert np.array_equal(dec.logits(), orc.logits)
+        assert nxt == ref
+        kk, vv = dec.kv_cache()
+        assert np.array_equal(kk[:, 8183], orc.bufs["key_cache"].reshape(k.shape)[:, 8183])
+        assert np.array_equal(vv[:, 8183], orc.bufs["value_cache"].reshape(v.shape)[:, 8183])
+        got = dec.generate_greedy(nxt, 8184, 8)
+        t, want = nxt, []
+        for i in range(8):
+            t = orc.forward(t, 8184 + i, oracle.GPU_ORDER)
+            want.append(t)
+        assert got == want
+        kk, vv = dec.kv_cache()
+        assert np.array_equal(kk[:, 8184:], orc.bufs["key_cache"].reshape(k.shape)[:, 8184:])
+        assert np.array_equal(vv[:, 8184:], orc.bufs["value_cache"].reshape(v.shape)[:, 8184:])
+        with pytest.raises(LlmError, match="past the kv cache size 8192"):
+            dec.forward(t, 8192)
+        with pytest.raises(LlmError, match="pass the kv cache size 8192"):
+            dec.generate_greedy(t, 8185, 8)
+    finally:
+        dec.close()
+
+
 @pytest.mark.parametrize("size", ["1.7B", "4B"])
 def test_persistent_step_wide_shapes_long_history(gpu, oracle, size):
     """The 1.7B and 4B specialisations of the persistent step (2 and 4 query heads per kv head)
