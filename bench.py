@@ -725,14 +725,15 @@ def config_decoder(size, n_prefill, steps):
     return dec, first, start, prompt, k, v
 
 
-def decode_config(size, n_prefill, steps, cpu_budget_s, read_peak=None):
+def decode_config(size, n_prefill, steps, cpu_budget_s, read_peak=None, compare_graph=False):
     """Greedy decode tokens/s of one more model config at batch 1: Qwen3-`size` shapes with the
     bench's seeded weights, either after a 5-token prompt or (n_prefill > 0) after a KV cache
     whose first n_prefill positions hold N(0, 1) keys and values (bf16 by truncation). `steps`
     tokens per generate call, the median of RUNS calls after a warm-up; the step is STEP_AUTO's
     (the persistent kernel below its switch position, the hipGraph of per-layer kernels from
     there on). With cpu_budget_s, the oracle decodes the same model from the same state for
-    about that long."""
+    about that long; with compare_graph, the hipGraph step decodes the same tokens too (its
+    tokens/s beside the line's)."""
     dec, first, start, prompt, k, v = config_decoder(size, n_prefill, steps)
     max_seq = dec.s.max_seq
     dt, _, walls, tokens = timed_runs(dec, first, start, steps, 8)
@@ -749,6 +750,13 @@ def decode_config(size, n_prefill, steps, cpu_budget_s, read_peak=None):
            "first_tokens": tokens[:4]}
     log(f"Qwen3-{size}: {out['tokens_per_s']} tokens/s ({out['step']}), "
         f"{out['effective_GB/s']} GB/s")
+    if compare_graph:
+        dec.capture_graph("graph")
+        gdt, _, _, gtokens = timed_runs(dec, first, start, steps, 8)
+        if gtokens != tokens:
+            raise RuntimeError("bench: the hipGraph step decoded other tokens")
+        out["graph_tokens_per_s"] = round(steps / gdt, 2)
+        log(f"  the same on the hipGraph step: {out['graph_tokens_per_s']} tokens/s")
     if cpu_budget_s:
         sys.path.insert(0, str(ROOT / "oracle"))
         import oracle
@@ -792,7 +800,8 @@ def main():
                     help="write /proc/self/maps to PATH just before exit (to name the mapped "
                          "object of a program counter a profiler reports after the run)")
     ap.add_argument("--no-configs", action="store_true",
-                    help="skip the Qwen3-1.7B and Qwen3-4B (8192-position cache) decode lines")
+                    help="skip the Qwen3-1.7B, Qwen3-4B (5-token prompt and 8192-position "
+                         "cache) and Qwen3-0.6B (8192-position cache) decode lines")
     ap.add_argument("--pmc-workload", nargs="?", const="0.6B", choices=["0.6B", "1.7B", "4B"],
                     help="only run the short counter-collection workload (one 256-token launch "
                          "of the step kernel; default size 0.6B)")
@@ -973,12 +982,16 @@ def run_bench(args):
     dec.close()
     if not args.no_configs:
         # the other decode configs of the metric: Qwen3-1.7B and Qwen3-4B after a 5-token prompt,
-        # and Qwen3-4B after an 8192-position cache (mean position 8320.5), 256 tokens each
+        # and Qwen3-4B after an 8192-position cache (mean position 8320.5), 256 tokens each; and
+        # Qwen3-0.6B after an 8192-position cache, where the step kernel's split attention runs
+        # (beside the hipGraph step on the same tokens)
         budget = 0 if args.no_cpu_baseline else 10.0
         line["decode_configs"] = {
             "qwen3_1.7B": decode_config("1.7B", 0, 256, budget, read_peak),
             "qwen3_4B": decode_config("4B", 0, 256, None, read_peak),
             "qwen3_4B_ctx8192": decode_config("4B", 8192, 256, budget, read_peak),
+            "qwen3_0.6B_ctx8192": decode_config("0.6B", 8192, 256, None, read_peak,
+                                                compare_graph=True),
         }
         line["fused_layer_4B"] = fused_layer_rate("4B", read_peak)
     print(json.dumps(line), flush=True)

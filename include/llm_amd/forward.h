@@ -132,6 +132,10 @@ typedef struct {
                                once per step for the in-scores attention of every layer */
     int step_switch_pos;    /* with the persistent kernel prepared: positions below this run it,
                                positions from it on the hipGraph step (set by capture_graph) */
+    int step_split_blocks;  /* the persistent kernel's attention runs one workgroup per query
+                               head below this many blocks of 64 positions of history, and split
+                               over (kv head, block) items from it on (1..128; set by
+                               capture_graph to the shapes' measured crossover) */
 } RunState;
 
 /* RunState::attn_mode. ATTN_AUTO takes ATTN_IN_SCORES when the longest history (max_seq) has at
@@ -147,13 +151,16 @@ enum { ATTN_AUTO = 0, ATTN_SEPARATE = 1, ATTN_IN_SCORES = 2, ATTN_ONE_PASS = 3 }
 
 /* How capture_graph prepares the step. STEP_AUTO: where the shapes have a specialisation
  * (Qwen3-0.6B, 1.7B, 4B), the persistent step kernel (one launch per forward;
- * generate_greedy runs its tokens in one launch) for the positions below
- * RunState::step_switch_pos, and a hipGraph of the per-layer kernels from there on: the kernel's
- * attention runs one workgroup per query head, so its cost grows with the history faster than
- * the graph's (crossover 736 / 512 / 480 positions at 0.6B / 1.7B / 4B; 5-token prompt: 2356 /
- * 1121 / 578 tokens/s against 1278 / 893 / 492). Other shapes: the hipGraph. STEP_GRAPH:
- * always the hipGraph. STEP_PERSISTENT: the persistent kernel at every position (max_seq at
- * most 8192) or an error. */
+ * generate_greedy runs its tokens in one launch, or two where they cross
+ * RunState::step_split_blocks) for the positions below RunState::step_switch_pos, and a
+ * hipGraph of the per-layer kernels from there on. The kernel's attention runs one workgroup
+ * per query head up to 448 / 512 / 512 positions at 0.6B / 1.7B / 4B, and split over
+ * (kv head, 64-position block) items on every workgroup from there on; the graph takes over
+ * where it is faster (1.7B and 4B from 5120 positions; 0.6B never, up to the kernel's longest
+ * history, 12288 positions on 256 CUs). 5-token prompt: 2356 / 1121 / 578 tokens/s against
+ * 1278 / 893 / 492 for the graph; 0.6B after 4096 positions 1374 against 1131. Other shapes:
+ * the hipGraph. STEP_GRAPH: always the hipGraph. STEP_PERSISTENT: the persistent kernel at
+ * every position (max_seq at most the kernel's longest history) or an error. */
 enum { STEP_AUTO = 0, STEP_GRAPH = 1, STEP_PERSISTENT = 2 };
 
 /* src/loader.cu:105-139 (config.json, generation_config.json) */

@@ -40,6 +40,8 @@ __device__ __forceinline__ void st16(void *p, u32x4 v) { *gptr((u32x4 *)p) = v; 
 constexpr int BUFFER_FLAGS = 0x00020000;
 // Cache policy operand of a buffer load: non-temporal, as ld16_nt.
 constexpr int BUFFER_NT = 2;
+// Cache policy operand of a buffer load with the coherence of an agent-scope atomic load (sc1).
+constexpr int BUFFER_SC1 = 16;
 
 // bf16 element e of a packed 16-byte chunk (element 0 in the low half of dword 0).
 __device__ __forceinline__ float lo_f(uint32_t w) { return __uint_as_float(w << 16); }

@@ -65,7 +65,7 @@ extern "C" void alloc_run_state_seq(RunState *s, const Config *cfg, int max_seq)
               dmalloc((void **)&s->next_token, 4) && dmalloc((void **)&s->pos, 4) &&
               dmalloc(&s->argmax_partials, (size_t)argmax_partial_count() * 8) &&
               dmalloc((void **)&s->pos_base, 4) && dmalloc((void **)&s->error_flag, 4) &&
-              dmalloc(&s->step_ws, step_workspace_bytes(cfg)) &&
+              dmalloc(&s->step_ws, step_workspace_bytes(cfg, max_seq)) &&
               dmalloc((void **)&s->rope_table, (size_t)cfg->head_dim * 4);
     if (ok && attention_one_pass_supported(cfg->n_heads, cfg->n_kv_heads, cfg->head_dim, max_seq))
         ok = dmalloc(&s->attn_one_pass_ws,
@@ -295,12 +295,13 @@ static bool prepare_persistent(const Config *cfg, const Weights *w, RunState *s)
     }
     const bool ok = HIP_OK(hipMemcpy(s->layers_dev, host, sizeof(LayerDev) * cfg->n_layers,
                                      hipMemcpyHostToDevice)) &&
-                    HIP_OK(hipMemset(s->step_ws, 0, step_workspace_bytes(cfg)));
+                    HIP_OK(hipMemset(s->step_ws, 0, step_workspace_bytes(cfg, s->max_seq)));
     free(host);
     if (!ok) return false;
     int grid = step_kernel_grid();
     if (grid <= 0) return llm_fail("capture_graph: cannot read the CU count");
     s->step_grid = grid > 1024 ? 1024 : grid;
+    s->step_split_blocks = step_kernel_split_blocks(cfg);
     s->persistent = 1;
     return true;
 }
@@ -330,6 +331,8 @@ static StepArgs step_args(const Config *cfg, const Weights *w, RunState *s, int 
     a.epoch = &ws->epoch;
     a.token_word = &ws->token_word;
     a.n_tokens = 1;
+    step_split_buffers(cfg, s->max_seq, s->step_ws, &a.tstat, &a.tpart);
+    a.max_blocks = step_split_max_blocks(cfg, s->max_seq);
     a.final_ctr = &ws->final_ctr;
     a.amax_val = ws->amax_val;
     a.amax_idx = ws->amax_idx;
@@ -353,7 +356,7 @@ static bool check_step_error(const Config *cfg, RunState *s) {
     if (!HIP_OK(hipMemcpy(&err, s->error_flag, 4, hipMemcpyDeviceToHost))) return false;
     if (err == 0) return true;
     HIP_OK(hipMemset(s->error_flag, 0, 4));
-    HIP_OK(hipMemset(s->step_ws, 0, step_workspace_bytes(cfg)));
+    HIP_OK(hipMemset(s->step_ws, 0, step_workspace_bytes(cfg, s->max_seq)));
     return llm_fail(err == 2 ? "step: a wait for another workgroup's data timed out"
                              : "step: token or position out of range on the device");
 }
@@ -401,6 +404,16 @@ static bool persistent_at(const RunState *s, int pos) {
     return s->persistent && pos < s->step_switch_pos;
 }
 
+// The first position whose step the persistent kernel runs with its split attention, or -1
+// (with an error) when RunState::step_split_blocks is outside 1..128.
+static int split_from(const RunState *s) {
+    if (s->step_split_blocks < 1 || s->step_split_blocks > 128) {
+        llm_fail("step: step_split_blocks %d outside 1..128", s->step_split_blocks);
+        return -1;
+    }
+    return (s->step_split_blocks - 1) * 64;
+}
+
 static bool check_token_pos(const Config *cfg, const RunState *s, int token, int pos) {
     if (token < 0 || token >= cfg->vocab_size)
         return llm_fail("forward: token %d outside vocab of %d", token, cfg->vocab_size);
@@ -418,7 +431,9 @@ extern "C" void forward(const Config *cfg, const Weights *w, RunState *s, int to
     if (dump_enabled()) {
         forward_kernels(cfg, w, s);  // the dumps come from the eager step (src/main.cu:253)
     } else if (persistent_at(s, pos)) {
-        if (step_kernel_launch(cfg, step_args(cfg, w, s, 0), s->step_grid, s->stream))
+        const int sp = split_from(s);
+        if (sp >= 0 &&
+            step_kernel_launch(cfg, step_args(cfg, w, s, 0), pos >= sp, s->step_grid, s->stream))
             s->next_token_valid = 1;
     } else if (s->graph) {
         HIP_OK(hipGraphLaunch(s->graph, s->stream));
@@ -525,9 +540,21 @@ extern "C" int generate_greedy(const Config *cfg, const Weights *w, RunState *s,
     set_token_pos_kernel<<<1, 64, 0, s->stream>>>(s->error_flag, s->pos_base, 0, pos);
     if (!LAUNCH_OK()) return -1;
     if (n_kernel > 0) {
+        // one launch decodes every token below the split attention's first position, one more
+        // every token from there to the switch (it continues from the token and position the
+        // first left on the device)
+        const int sp = split_from(s);
+        if (sp < 0) return -1;
+        const int n_heads = pos >= sp ? 0 : pos + n_kernel <= sp ? n_kernel : sp - pos;
         StepArgs a = step_args(cfg, w, s, 1);
-        a.n_tokens = n_kernel;  // one launch decodes every token below the switch
-        if (!step_kernel_launch(cfg, a, s->step_grid, s->stream)) return -1;
+        if (n_heads > 0) {
+            a.n_tokens = n_heads;
+            if (!step_kernel_launch(cfg, a, false, s->step_grid, s->stream)) return -1;
+        }
+        if (n_heads < n_kernel) {
+            a.n_tokens = n_kernel - n_heads;
+            if (!step_kernel_launch(cfg, a, true, s->step_grid, s->stream)) return -1;
+        }
     }
     for (int i = n_kernel; i < n_steps; i++)
         if (!HIP_OK(hipGraphLaunch(s->loop_graph, s->stream))) return -1;

@@ -38,6 +38,10 @@ struct StepArgs {
     float eps, scale;
     int n_layers, vocab, max_seq, token_capacity, advance;
     int n_tokens;  // decode steps this launch runs (each feeds its argmax to the next)
+    // The split instance's tagged block statistics [n_heads, max_blocks, 2] (max, sum) and
+    // block partials [n_heads, max_blocks, head_dim], 64-bit words (float bits << 32) | tag.
+    unsigned long long *tstat, *tpart;
+    int max_blocks;
     float inv_freq[64];
 };
 
@@ -52,13 +56,29 @@ struct StepWorkspace {
     int amax_idx[1024];
 };
 
-size_t step_workspace_bytes(const Config *cfg);
+// The workspace for a run state of max_seq positions: the words above, the tagged vectors, then
+// the split attention's statistics and partials.
+size_t step_workspace_bytes(const Config *cfg, int max_seq);
+// Blocks of 64 positions the split attention's workspace holds for max_seq positions, and where
+// its statistics and partials sit in the workspace `ws`.
+int step_split_max_blocks(const Config *cfg, int max_seq);
+void step_split_buffers(const Config *cfg, int max_seq, void *ws, unsigned long long **tstat,
+                        unsigned long long **tpart);
 // STEP_PERSISTENT: the shapes have a specialisation and every position fits its attention.
 bool step_kernel_supported(const Config *cfg, int max_seq);
+// The positions the step kernel's attention can hold at most (one workgroup per query head
+// below the split, split items above it).
+int step_kernel_max_seq(const Config *cfg);
+// The history (blocks of 64 positions) from which the shapes' step kernel splits attention over
+// (kv head, block) items: the measured crossover of the two attention forms.
+int step_kernel_split_blocks(const Config *cfg);
 // The shapes have a specialisation (STEP_AUTO then runs it below step_kernel_switch_pos).
 bool step_kernel_available(const Config *cfg);
-// The first position at which STEP_AUTO runs the hipGraph step instead of the step kernel
-// (whose one workgroup per query head makes attention cost grow with the history faster).
+// The first position at which STEP_AUTO runs the hipGraph step instead of the step kernel (the
+// measured crossover, at most the kernel's longest history).
 int step_kernel_switch_pos(const Config *cfg);
 int step_kernel_grid();
-bool step_kernel_launch(const Config *cfg, const StepArgs &args, int grid, hipStream_t stream);
+// Launches the step kernel; with `split` the instance whose attention runs split over (kv head,
+// block) items (long histories), else one workgroup per query head.
+bool step_kernel_launch(const Config *cfg, const StepArgs &args, bool split, int grid,
+                        hipStream_t stream);

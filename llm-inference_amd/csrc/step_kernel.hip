@@ -467,6 +467,42 @@ __device__ __forceinline__ int value_slot(int c0, int j, int it) {
     return (c0 + (w >> 2) + 2 * j) * 64 + (w & 3) * 16 + it * 4 + ((tid_x() & 63) >> 4);
 }
 
+// QK-RMSNorm + RoPE of one 128-element head by one wave (qk_norm_rope_kernel arithmetic): lane
+// i holds elements i and i + 64 of x16 (bf16 bits), the pair RoPE rotates with table entry i
+// (c, sn), w0 / w1 the norm weights of those elements; lanes 0-7 form the sum of squares in the
+// order of the standalone kernel (elements 8L.. then 64+8L.., then the 8-lane tree). oa / ob:
+// the rotated elements i and i + 64 (bf16 bits).
+__device__ __forceinline__ void wave_qk_norm_rope(const uint16_t *x16, uint32_t w0, uint32_t w1,
+                                                  float c, float sn, float eps, uint32_t &oa,
+                                                  uint32_t &ob) {
+    constexpr int D = 128;
+    const int lane = tid_x() & 63;
+    const uint32_t xi = x16[lane], xj = x16[64 + lane];
+    float acc = 0.0f;
+    {
+        const int L8 = (lane & 7) * 8;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float v = bf2f((bf16)x16[L8 + e]);
+            acc = fmaf(v, v, acc);
+        }
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float v = bf2f((bf16)x16[64 + L8 + e]);
+            acc = fmaf(v, v, acc);
+        }
+    }
+    const float total = __uint_as_float(
+        __builtin_amdgcn_readfirstlane(__float_as_uint(group_sum<8>(acc))));
+    const float inv = 1.0f / sqrtf(total / (float)D + eps);
+    const float ya = round_bf(round_bf(bf2f((bf16)xi) * inv) * bf2f((bf16)w0));
+    const float yb = round_bf(round_bf(bf2f((bf16)xj) * inv) * bf2f((bf16)w1));
+    const float a_cos = round_bf(ya * c), b_sin = round_bf(yb * sn);
+    const float b_cos = round_bf(yb * c), a_sin = round_bf(ya * sn);
+    oa = f2bf(a_cos - b_sin);
+    ob = f2bf(b_cos + a_sin);
+}
+
 template <class S>
 __device__ __forceinline__ void attention_prefetch(KArgs &a, KLayer &L, int h, int pos, int pos0,
                                                    int layer, AttnPrefetch &p) {
@@ -557,29 +593,8 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
         const uint32_t xi = x16[lane], xj = x16[64 + lane];
         const size_t row = (size_t)pos * KVD + g * D;
         if (w < 2) {
-            float acc = 0.0f;
-            {
-                const int L8 = (lane & 7) * 8;
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const float v = bf2f((bf16)x16[L8 + e]);
-                    acc = fmaf(v, v, acc);
-                }
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const float v = bf2f((bf16)x16[64 + L8 + e]);
-                    acc = fmaf(v, v, acc);
-                }
-            }
-            const float total = __uint_as_float(
-                __builtin_amdgcn_readfirstlane(__float_as_uint(group_sum<8>(acc))));
-            const float inv = 1.0f / sqrtf(total / (float)D + a.eps);
-            const float ya = round_bf(round_bf(bf2f((bf16)xi) * inv) * bf2f((bf16)pre.w0));
-            const float yb = round_bf(round_bf(bf2f((bf16)xj) * inv) * bf2f((bf16)pre.w1));
-            const float c = pre.cs[0], sn = pre.sn[0];
-            const float a_cos = round_bf(ya * c), b_sin = round_bf(yb * sn);
-            const float b_cos = round_bf(yb * c), a_sin = round_bf(ya * sn);
-            const uint32_t oa = f2bf(a_cos - b_sin), ob = f2bf(b_cos + a_sin);
+            uint32_t oa, ob;
+            wave_qk_norm_rope(x16, pre.w0, pre.w1, pre.cs[0], pre.sn[0], a.eps, oa, ob);
             uint16_t *dst = (uint16_t *)(w == 0 ? sm.q : sm.k);
             dst[lane] = (uint16_t)oa;
             dst[64 + lane] = (uint16_t)ob;
@@ -773,6 +788,445 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
     if (threadIdx.x < D) put_tagged_all<QD, S::REPLICAS>(a.tattn, h * D + threadIdx.x, f2bf(out_d), tag_out);
 }
 
+// ---------------------------------------------------------------- split attention
+
+// Long histories: attention split over (kv head g, 64-position block b) items, each run by half
+// a workgroup (waves 4h..4h+3, 256 threads) with the lane layout and arithmetic of the
+// multi-kernel step's passes (attn_scores_kernel, pv_item, the block-order combine), so the
+// results are those of that step bit for bit. Half-slot s = 2 * workgroup + h takes kv head
+// s % HKV and blocks s / HKV + k * SPG, k < SPLIT_ITEMS (SPG = 2 * grid / HKV half-slots per kv
+// head; the host checks that the history fits). An item publishes its query heads' block
+// statistics (max, sum of exp(s - max)) and, once every block's statistics of its kv head are
+// in, its heads' block partials of p v, as tagged 64-bit words (float bits << 32 | tag); the
+// last 2 HQ workgroups of the grid (which own no o rows) then each add the partials of half a
+// head's columns in block order and publish them. Every workgroup takes part: its items' key
+// and value rows are requested before it polls the q/k/v vector, so the history streams on
+// every CU at once.
+constexpr int SPLIT_ITEMS = 3;   // items of a half-slot at most
+constexpr int SPLIT_MAXB = 192;  // blocks of 64 positions at most (3 chunks of 64 statistics)
+constexpr int COMB_COLS = 64;    // columns of a head one workgroup combines
+
+template <class S>
+struct SplitSmem {
+    static constexpr int REP = S::HQ / S::HKV, D = 128;
+    uint32_t raw[2][REP + 2][D / 2];    // each half's q heads, k and v as polled (bf16 pairs)
+    u32x4 q[2][REP][D / 8];             // roped query heads
+    u32x4 k[2][D / 8];                  // roped key at pos
+    float sc[2][SPLIT_ITEMS][REP][64];  // scores, then probabilities
+    float gst[2][REP][2];               // each head's global max and sum
+    float red[2][4][REP][D];            // the four waves' PV partials
+    float comb[SPLIT_MAXB][COMB_COLS];  // a combine's staged block partials
+};
+
+// The key and value history rows of a half-slot's items, this lane's chunks (rows at or past
+// pos read as zeros), requested a phase ahead of their use.
+struct SplitKV {
+    u32x4 k[SPLIT_ITEMS][4], v[SPLIT_ITEMS][4];
+};
+
+// Where a half-slot's items lie: kv head g, first block j0, SPG blocks apart; n_it items for the
+// workgroup's loop (half 0 has at least as many as half 1). Half h of workgroup w is half-slot
+// h * grid + w, so where some half-slots take one item more than the others (histories of
+// more than 2 SPG blocks), those are half 0 of as many workgroups, not both halves of half as
+// many: a CU then has one item less to compute.
+struct SplitItems {
+    int g, j0, spg, n_it;
+};
+template <class S>
+__device__ __forceinline__ SplitItems split_items(int nb) {
+    SplitItems it;
+    it.spg = 2 * (int)gridDim.x / S::HKV;
+    const int hslot = (wave_id() >> 2) * (int)gridDim.x + (int)blockIdx.x;
+    it.g = hslot % S::HKV;
+    it.j0 = hslot / S::HKV;
+    const int j00 = (int)blockIdx.x / S::HKV;
+    it.n_it = j00 < nb ? min(SPLIT_ITEMS, (nb - 1 - j00) / it.spg + 1) : 0;
+    return it;
+}
+
+// Requests the history rows of this workgroup's items of layer `layer` at `pos` (slot
+// w4 * 16 + it * 4 + G of each block, lane chunk Lk); rows written during this launch
+// (t >= pos0) coherently.
+template <class S>
+__device__ __forceinline__ void split_request(KArgs &a, int pos, int pos0, int layer, SplitKV &kv) {
+    constexpr int D = 128, KVD = S::HKV * D;
+    const int nb = (pos + 64) / 64;
+    const SplitItems si = split_items<S>(nb);
+    const int lane = tid_x() & 63, w4 = wave_id() & 3, G = lane >> 4, Lk = lane & 15;
+    const bf16 *kc = a.key_cache + (size_t)layer * a.max_seq * KVD;
+    const bf16 *vc = a.value_cache + (size_t)layer * a.max_seq * KVD;
+    const u32x4 zero{0, 0, 0, 0};
+#pragma unroll
+    for (int k = 0; k < SPLIT_ITEMS; k++)
+#pragma unroll
+        for (int it = 0; it < 4; it++) {
+            const int t = (si.j0 + k * si.spg) * 64 + w4 * 16 + it * 4 + G;
+            const bool in = k < si.n_it && t < pos;
+            const size_t off = (size_t)t * KVD + si.g * D + 8 * Lk;
+            kv.k[k][it] = in ? ld_kv(kc + off, t, pos0) : zero;
+            kv.v[k][it] = in ? ld_kv(vc + off, t, pos0) : zero;
+        }
+}
+
+__device__ __forceinline__ void put_tagged64(unsigned long long *p, float v, uint32_t tag) {
+    __hip_atomic_store(gptr(p), ((unsigned long long)__float_as_uint(v) << 32) | tag,
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Polls the tagged 64-bit words src(i), i < count (count >= 1), thread t taking i = t + T j
+// (j < P), until every tag is `tag`, then hands each value to dst(i, v). Lanes past the count
+// re-read the last word, so no branch surrounds a load. Bounded as stage_pairs.
+template <int P, int T, class Src, class Dst>
+__device__ __forceinline__ void poll_tagged64(int t, int count, uint32_t tag, int *err, Src src,
+                                              Dst dst) {
+    uint64_t w[P];
+    long long spins = 0;
+    for (;;) {
+        bool fresh = true;
+#pragma unroll
+        for (int j = 0; j < P; j++) {
+            w[j] = ld_coh64(src(min(t + T * j, count - 1)));
+            fresh &= (uint32_t)w[j] == tag;
+        }
+        if (fresh) break;
+        if ((++spins & 63) == 0 && wait_gives_up(spins, SPIN_LIMIT, err)) break;
+    }
+#pragma unroll
+    for (int j = 0; j < P; j++)
+        if (t + T * j < count) dst(t + T * j, __uint_as_float((uint32_t)(w[j] >> 32)));
+}
+
+// The split attention of layer `layer` at `pos` (n = pos + 1 > 0 positions, at most
+// SPLIT_ITEMS * SPG blocks): q/k/v polled with tag `tag_in`; statistics, partials and, on the
+// combining workgroups, the output published with `tag_out`. cs / sn: this lane's RoPE table
+// entry at pos.
+template <class S>
+__device__ __forceinline__ void split_attention(KArgs &a, KLayer &L, int pos, int layer,
+                                                SplitSmem<S> &sm, const SplitKV &kv,
+                                                uint32_t tag_in, uint32_t tag_out, float cs,
+                                                float sn, int n_layers, int step) {
+    constexpr int D = 128, REP = S::HQ / S::HKV, QD = S::HQ * D, KVD = S::HKV * D;
+    static_assert(REP >= 1 && REP <= 4, "query heads per kv head");
+    const int n = pos + 1, nb = (n + 63) / 64, mb = a.max_blocks;
+    const int lane = tid_x() & 63, hf = wave_id() >> 2, w4 = wave_id() & 3;
+    const int ht = tid_x() & 255;  // thread of the half
+    const int G = lane >> 4, Lk = lane & 15;
+    const SplitItems si = split_items<S>(nb);
+    const int spg = si.spg, g = si.g, j0 = si.j0, n_it = si.n_it;
+    bf16 *kc = a.key_cache + (size_t)layer * a.max_seq * KVD;
+    bf16 *vc = a.value_cache + (size_t)layer * a.max_seq * KVD;
+    if (n_it > 0) {
+        // (the items' history rows were requested with split_request; loads complete in order,
+        // so the q/k/v poll below lands once they have)
+        uint32_t qn0, qn1, kn0, kn1;
+        {
+            const uint16_t *qn = (const uint16_t *)L.q_norm, *kn = (const uint16_t *)L.k_norm;
+            qn0 = gptr(qn)[lane];
+            qn1 = gptr(qn)[64 + lane];
+            kn0 = gptr(kn)[lane];
+            kn1 = gptr(kn)[64 + lane];
+        }
+        // the half's q heads, k and v (every half polls its own kv head's words)
+        __syncthreads();
+        {
+            constexpr int PAIRS = (REP + 2) * D / 2, PP = (PAIRS + 255) / 256;
+            const uint32_t *tq = a.tqkv;
+            uint32_t *dst = &sm.raw[hf][0][0];
+            uint64_t wd[PP];
+            long long spins = 0;
+            for (;;) {
+                bool fresh = true;
+#pragma unroll
+                for (int j = 0; j < PP; j++) {
+                    const int p = min(ht + 256 * j, PAIRS - 1);
+                    const int seg = p / (D / 2), i = 2 * (p % (D / 2));
+                    const int off = seg < REP ? (g * REP + seg) * D
+                                              : QD + (seg - REP) * KVD + g * D;
+                    wd[j] = ld_coh64(tq + off + i);
+                    fresh &= (uint32_t)(wd[j] & 0xffffu) == tag_in &&
+                             (uint32_t)((wd[j] >> 32) & 0xffffu) == tag_in;
+                }
+                if (fresh) break;
+                if ((++spins & 63) == 0 && wait_gives_up(spins, SPIN_LIMIT, a.error_flag)) break;
+            }
+#pragma unroll
+            for (int j = 0; j < PP; j++) {
+                const int p = ht + 256 * j;
+                if (p < PAIRS)
+                    dst[p] = (uint32_t)((wd[j] >> 16) & 0xffffu) | ((uint32_t)(wd[j] >> 48) << 16);
+            }
+        }
+        __syncthreads();
+        if (blockIdx.x < S::HQ) stamp_wg(layer, n_layers, 0, step);
+        // QK-norm + RoPE of the query heads (wave r of the half: head r) and, in the half whose
+        // items hold pos, of the key, which that half writes with the value into row pos
+        const int pb = nb - 1;  // the block holding pos
+        const bool has_pos = pb >= j0 && (pb - j0) % spg == 0;
+        for (int hh = w4; hh < REP + (has_pos ? 1 : 0); hh += 4) {
+            const bool is_k = hh == REP;
+            uint32_t oa, ob;
+            wave_qk_norm_rope((const uint16_t *)sm.raw[hf][hh], is_k ? kn0 : qn0,
+                              is_k ? kn1 : qn1, cs, sn, a.eps, oa, ob);
+            uint16_t *dst = (uint16_t *)(is_k ? sm.k[hf] : sm.q[hf][hh]);
+            dst[lane] = (uint16_t)oa;
+            dst[64 + lane] = (uint16_t)ob;
+            if (is_k) {
+                const size_t row = (size_t)pos * KVD + g * D;
+                st_kv(kc + row + lane, oa);
+                st_kv(kc + row + 64 + lane, ob);
+            }
+        }
+        if (has_pos && w4 == 3) {
+            const uint16_t *v16 = (const uint16_t *)sm.raw[hf][REP + 1];
+            const size_t row = (size_t)pos * KVD + g * D;
+            st_kv(vc + row + lane, v16[lane]);
+            st_kv(vc + row + 64 + lane, v16[64 + lane]);
+        }
+        __syncthreads();
+        // scores s = bf16(bf16(q.k) * scale) of each item (attn_scores_kernel layout: slot
+        // w4 * 16 + it * 4 + G, 16 lanes per position, reduce-scattered)
+        {
+            constexpr int NP = 4 * REP, SL = NP < 16 ? NP : 16;
+            // the query heads' chunks as fp32 once (bf16 -> fp32 is exact, so each product and
+            // the order of the fmas are those of dot8)
+            float qf[REP][8];
+#pragma unroll
+            for (int r = 0; r < REP; r++) {
+                const u32x4 qv = sm.q[hf][r][Lk];
+#pragma unroll
+                for (int e = 0; e < 8; e++) qf[r][e] = elem(qv, e);
+            }
+            const u32x4 kcur = sm.k[hf][Lk];
+#pragma unroll
+            for (int k = 0; k < SPLIT_ITEMS; k++) {
+                const int b = j0 + k * spg;
+                if (k >= n_it) break;
+                if (b >= nb) continue;
+                float part[NP];
+#pragma unroll
+                for (int it = 0; it < 4; it++) {
+                    const int t = b * 64 + w4 * 16 + it * 4 + G;
+                    const u32x4 kt = t == pos ? kcur : kv.k[k][it];
+                    float kf[8];
+#pragma unroll
+                    for (int e = 0; e < 8; e++) kf[e] = elem(kt, e);
+#pragma unroll
+                    for (int r = 0; r < REP; r++) {
+                        float d = 0.0f;
+#pragma unroll
+                        for (int e = 0; e < 8; e++) d = fmaf(qf[r][e], kf[e], d);
+                        part[it * REP + r] = d;
+                    }
+                }
+#pragma unroll
+                for (int s0 = 0; s0 < NP; s0 += SL) {
+                    float slice[SL];
+#pragma unroll
+                    for (int j = 0; j < SL; j++) slice[j] = part[s0 + j];
+                    const float d = group_sum_scatter<16, SL>(slice);
+                    const int j = s0 + scatter_row<SL>(Lk), it = j / REP, r = j - it * REP;
+                    if (Lk < SL) sm.sc[hf][k][r][w4 * 16 + it * 4 + G] = round_bf(round_bf(d) * a.scale);
+                }
+            }
+        }
+        __syncthreads();
+        // block statistics (wave r of the half: head r), published
+        if (w4 < REP) {
+            const int h = g * REP + w4;
+#pragma unroll
+            for (int k = 0; k < SPLIT_ITEMS; k++) {
+                const int b = j0 + k * spg;
+                if (k >= n_it) break;
+                if (b >= nb) continue;
+                const bool v = b * 64 + lane < n;
+                const float sv = v ? sm.sc[hf][k][w4][lane] : -__builtin_huge_valf();
+                const float m = wave_max(sv);
+                const float e = v ? exp_f32(sv - m) : 0.0f;
+                const float ssum = wave_sum(e);
+                if (lane == 0) {
+                    unsigned long long *st = a.tstat + ((size_t)h * mb + b) * 2;
+                    put_tagged64(st, m, tag_out);
+                    put_tagged64(st + 1, ssum, tag_out);
+                }
+            }
+        }
+        // every block's statistics of the head: global max M (exact in any order) and sum (the
+        // chunks of 64 blocks tree-summed, S_b exp(m_b - M), added in order)
+        if (w4 < REP && j0 < nb) {
+            constexpr int MAXC = SPLIT_MAXB / 64;
+            const unsigned long long *st = a.tstat + (size_t)(g * REP + w4) * mb * 2;
+            float mv[MAXC], sv[MAXC];
+            uint64_t wm[MAXC], ws[MAXC];
+            long long spins = 0;
+            for (;;) {
+                bool fresh = true;
+#pragma unroll
+                for (int c = 0; c < MAXC; c++) {
+                    const int bi = min(c * 64 + lane, nb - 1);
+                    wm[c] = ld_coh64(st + 2 * bi);
+                    ws[c] = ld_coh64(st + 2 * bi + 1);
+                    fresh &= (uint32_t)wm[c] == tag_out && (uint32_t)ws[c] == tag_out;
+                }
+                if (fresh) break;
+                if ((++spins & 63) == 0 && wait_gives_up(spins, SPIN_LIMIT, a.error_flag)) break;
+            }
+#pragma unroll
+            for (int c = 0; c < MAXC; c++) {
+                mv[c] = __uint_as_float((uint32_t)(wm[c] >> 32));
+                sv[c] = __uint_as_float((uint32_t)(ws[c] >> 32));
+            }
+            float ml = -__builtin_huge_valf();
+#pragma unroll
+            for (int c = 0; c < MAXC; c++) ml = c * 64 + lane < nb ? fmaxf(ml, mv[c]) : ml;
+            const float M = wave_max(ml);
+            float sum = 0.0f;
+#pragma unroll
+            for (int c = 0; c < MAXC; c++) {
+                if (c * 64 >= nb) break;
+                const float cs_ = wave_sum(c * 64 + lane < nb ? sv[c] * exp_f32(mv[c] - M) : 0.0f);
+                sum = c == 0 ? cs_ : sum + cs_;
+            }
+            if (lane == 0) {
+                sm.gst[hf][w4][0] = M;
+                sm.gst[hf][w4][1] = sum;
+            }
+        }
+        __syncthreads();
+        // probabilities p = bf16(exp(s - M) / sum)
+        if (w4 < REP) {
+            const float M = sm.gst[hf][w4][0], sum = sm.gst[hf][w4][1];
+#pragma unroll
+            for (int k = 0; k < SPLIT_ITEMS; k++) {
+                const int b = j0 + k * spg;
+                if (k >= n_it) break;
+                if (b >= nb) continue;
+                const float sv = sm.sc[hf][k][w4][lane];
+                sm.sc[hf][k][w4][lane] = b * 64 + lane < n ? round_bf(exp_f32(sv - M) / sum) : 0.0f;
+            }
+        }
+        __syncthreads();
+        // PV of each item (pv_item layout: per lane over its slots in order, the position
+        // groups reduce-scattered with the butterfly's pairing, the four waves added in order),
+        // published per head and element
+        const u32x4 vcur = ((const u32x4 *)sm.raw[hf][REP + 1])[Lk];
+        // the KV row this workgroup may have stored is complete before any partial that later
+        // steps depend on is published
+        __builtin_amdgcn_s_waitcnt(0);
+#pragma unroll
+        for (int k = 0; k < SPLIT_ITEMS; k++) {
+            if (k >= n_it) break;
+            const int b = j0 + k * spg;
+            if (b < nb) {
+                float acc[REP][8];
+#pragma unroll
+                for (int r = 0; r < REP; r++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) acc[r][e] = 0.0f;
+#pragma unroll
+                for (int it = 0; it < 4; it++) {
+                    const int slot = w4 * 16 + it * 4 + G;
+                    const int t = b * 64 + slot;
+                    if (t < n) {
+                        const u32x4 vt = t == pos ? vcur : kv.v[k][it];
+#pragma unroll
+                        for (int r = 0; r < REP; r++) {
+                            const float p = sm.sc[hf][k][r][slot];
+#pragma unroll
+                            for (int e = 0; e < 8; e++) acc[r][e] = fmaf(p, elem(vt, e), acc[r][e]);
+                        }
+                    }
+                }
+                constexpr int NV = REP * 8, KEEP = NV / 4;
+                float flat[NV], kept[KEEP];
+#pragma unroll
+                for (int r = 0; r < REP; r++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) flat[r * 8 + e] = acc[r][e];
+                scatter_keep<NV, 16, 64>(flat, kept);
+                int off = 0;
+#pragma unroll
+                for (int q = 0, m = NV; (16 << q) < 64; q++, m >>= 1)
+                    if ((lane >> q) & 16) off += m / 2;
+#pragma unroll
+                for (int j = 0; j < KEEP; j++) {
+                    const int idx = off + j, r = idx / 8, e = idx % 8;
+                    sm.red[hf][w4][r][8 * Lk + e] = kept[j];
+                }
+            }
+            __syncthreads();
+            if (b < nb) {
+                for (int i = ht; i < REP * D; i += 256) {
+                    const int r = i / D, d = i - r * D;
+                    const float v = ((sm.red[hf][0][r][d] + sm.red[hf][1][r][d]) +
+                                     sm.red[hf][2][r][d]) +
+                                    sm.red[hf][3][r][d];
+                    put_tagged64(a.tpart + ((size_t)(g * REP + r) * mb + b) * D + d, v, tag_out);
+                }
+            }
+            __syncthreads();  // red is rewritten by the next item
+        }
+    }
+    // the last 2 HQ workgroups: columns [c0, c0 + COMB_COLS) of query head h, out = bf16(block
+    // partials added in block order), every block's partials polled at once
+    const int task = (int)blockIdx.x - ((int)gridDim.x - S::HQ * (D / COMB_COLS));
+    if (task >= 0) {
+        const int h = task / (D / COMB_COLS), c0 = (task % (D / COMB_COLS)) * COMB_COLS;
+        // thread t reads column t % 64 of blocks t / 64 + 8 j, as buffer loads with one lane
+        // offset (the block stride in the scalar offset) and the coherence of ld_coh64 (sc1);
+        // blocks past the history read as 0 and are not waited for
+        constexpr int BPJ = THREADS / COMB_COLS, P = SPLIT_MAXB / BPJ;
+        const int tb = tid_x() / COMB_COLS, tc = tid_x() % COMB_COLS;
+        const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+            (void *)(a.tpart + (size_t)h * mb * D + c0), (short)0, nb * D * 8, BUFFER_FLAGS);
+        const int voff = (tb * D + tc) * 8;
+        __syncthreads();
+        // first the column-c0 word of every block (one per thread; an item stores all its words
+        // at once): re-reading every partial while most are still being written would stream
+        // the whole set once per poll round
+        if ((int)threadIdx.x < nb) {
+            const unsigned long long *w0 = a.tpart + ((size_t)h * mb + threadIdx.x) * D + c0;
+            long long spins = 0;
+            while ((uint32_t)ld_coh64(w0) != tag_out)
+                if ((++spins & 63) == 0 && wait_gives_up(spins, SPIN_LIMIT, a.error_flag)) break;
+        }
+        __syncthreads();
+        {
+            uint64_t w[P];
+            long long spins = 0;
+            for (;;) {
+                bool fresh = true;
+#pragma unroll
+                for (int j = 0; j < P; j++) {
+                    const auto v = __builtin_amdgcn_raw_buffer_load_b64(rs, voff, j * BPJ * D * 8,
+                                                                        BUFFER_SC1);
+                    w[j] = ((uint64_t)v[1] << 32) | v[0];
+                    fresh &= tb + BPJ * j >= nb || (uint32_t)w[j] == tag_out;
+                }
+                if (fresh) break;
+                if ((++spins & 63) == 0 && wait_gives_up(spins, SPIN_LIMIT, a.error_flag)) break;
+            }
+#pragma unroll
+            for (int j = 0; j < P; j++)
+                if (tb + BPJ * j < nb) sm.comb[tb + BPJ * j][tc] = __uint_as_float((uint32_t)(w[j] >> 32));
+        }
+        __syncthreads();
+        if (threadIdx.x < COMB_COLS) {
+            const int c = threadIdx.x;
+            float acc = sm.comb[0][c];
+            int j = 1;
+            for (; j + 16 <= nb; j += 16) {  // 16 LDS reads in flight, then the adds
+                float v[16];
+#pragma unroll
+                for (int u = 0; u < 16; u++) v[u] = sm.comb[j + u][c];
+#pragma unroll
+                for (int u = 0; u < 16; u++) acc += v[u];
+            }
+            for (; j < nb; j++) acc += sm.comb[j][c];
+            put_tagged_all<QD, S::REPLICAS>(a.tattn, h * D + c0 + c, f2bf(acc), tag_out);
+        }
+    }
+}
+
 // ---------------------------------------------------------------- the step
 
 // Rows [r0, r1) of a phase with R rows owned by wave w of this workgroup, the rows spread in
@@ -828,13 +1282,16 @@ enum {
 // The roles a token loop is compiled for.
 enum { ROLE_ATTN = 0, ROLE_MATRIX = 1, ROLE_EITHER = 2 };
 
-template <class S>
+// SPLIT: the instance for long histories, whose attention runs split over (kv head, block)
+// items on every workgroup (split_attention); otherwise one workgroup per query head.
+template <class S, bool SPLIT>
 __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
     constexpr int H = S::H, I = S::I, D = 128, QD = S::HQ * D, KVD = S::HKV * D;
     constexpr int NCH = H / 512, NCO = QD / 512, NCI = I / 512;
     constexpr int VEC_WORDS = (I > QD ? (I > H ? I : H) : (QD > H ? QD : H)) / 2;
     __shared__ union Smem {
         AttnSmem<S> attn;
+        std::conditional_t<SPLIT, SplitSmem<S>, char> split;  // the split instance's only
         uint32_t vec[VEC_WORDS];  // the staged input vector of a matrix phase (bf16 pairs)
     } sm;
     __shared__ float red_v[WAVES];
@@ -852,8 +1309,15 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
         pos = *gptr(a.pos);
         n_layers = a.n_layers;
         n_tokens = a.n_tokens;
-        if (pos < 0 || n_tokens < 1 || pos + n_tokens > a.max_seq || pos + n_tokens > S::NMAX ||
-            token < 0 || token >= a.vocab) {
+        // one workgroup per query head holds at most NMAX positions; the split attention at
+        // most SPLIT_ITEMS items per half-slot and the blocks the workspace holds
+        const int last_nb = (pos + n_tokens + 63) / 64;
+        if (pos < 0 || n_tokens < 1 || pos + n_tokens > a.max_seq || token < 0 ||
+            token >= a.vocab ||
+            (SPLIT ? last_nb > a.max_blocks || last_nb > SPLIT_MAXB ||
+                         (2 * (int)gridDim.x) % S::HKV != 0 ||
+                         last_nb > SPLIT_ITEMS * (2 * (int)gridDim.x / S::HKV)
+                   : pos + n_tokens > S::NMAX)) {
             if (blockIdx.x == 0 && threadIdx.x == 0) *gptr(a.error_flag) = 1;
             return;  // every workgroup reads the same values and leaves at once
         }
@@ -941,8 +1405,24 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
     // after down, with seq = sq0 + PHASES * l; the next token: sq0 + PHASES * n_layers
     if (attn) {
         // ---- QK-norm + RoPE + KV write + attention, one query head per workgroup
+        float rope_c = 0.0f, rope_s = 0.0f;  // this lane's RoPE table entry at pos (split)
+        if constexpr (SPLIT) {
+            float cs[1], sn[1];
+            rope_table<D>(pos, kargs().inv_freq, cs, sn);
+            rope_c = cs[0];
+            rope_s = sn[0];
+        }
         for (int l = 0; l < n_layers; l++) {
             const unsigned seq = sq0 + PHASES * l;
+            if constexpr (SPLIT) {
+                KArgs &a = kargs();
+                SplitKV kv;
+                split_request<S>(a, opaque(pos), opaque(pos0), l, kv);
+                split_attention<S>(a, klayer(a, l), opaque(pos), l, sm.split, kv, tag_of(seq),
+                                   tag_of(seq + 1), rope_c, rope_s, n_layers, step);
+                stamp_wg(l, n_layers, 1, step);
+                continue;
+            }
             for (int h = blockIdx.x; h < S::HQ; h += gridDim.x) {
                 KArgs &a = kargs();
                 AttnPrefetch pre;
@@ -953,6 +1433,13 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
             }
         }
     } else {
+        float rope_c = 0.0f, rope_s = 0.0f;  // this lane's RoPE table entry at pos (split)
+        if constexpr (SPLIT) {
+            float cs[1], sn[1];
+            rope_table<D>(pos, kargs().inv_freq, cs, sn);
+            rope_c = cs[0];
+            rope_s = sn[0];
+        }
         // the wave's residual rows of x (lane j: row o0 + j), starting as the embedding row
         uint32_t xown = 0;
         if (o0 < o1) {
@@ -974,6 +1461,10 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
             }
             stamp<S>(1 + 4 * l, step);
             stamp_wg(l, n_layers, 0, step);
+            // long histories: this workgroup's key and value rows of the split attention, which
+            // stream during the q/k/v rows (its q/k/v stores then complete after them)
+            SplitKV kv;
+            if constexpr (SPLIT) split_request<S>(kargs(), opaque(pos), opaque(pos0), l, kv);
             if (wg_q) wg_rmsnorm<H>(sm.vec, nq, kargs().eps, &norm_inv);
             if (q0 < q1) {
                 KArgs &a = kargs();
@@ -995,15 +1486,30 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
             Rows<NCH, S::B_GU> pf_g{}, pf_u{};
             Rows<NCI, S::B_DOWN> pf_d{};
             NormW<H> ng{};  // mlp_norm weights
-            pf_o.load(o_row(klayer(kargs(), l)), o0, o1);
-            ng.load(klayer(kargs(), l).mlp_norm);
-            {
-                KLayer &L = klayer(kargs(), l);
-                const bf16 *wg = L.w_gate, *wu = L.w_up;
-                pf_g.load([=](int r) { return wg + (size_t)r * H; }, g0, g1);
-                pf_u.load([=](int r) { return wu + (size_t)r * H; }, g0, g1);
+            auto prefetch = [&]() __attribute__((always_inline)) {
+                pf_o.load(o_row(klayer(kargs(), l)), o0, o1);
+                ng.load(klayer(kargs(), l).mlp_norm);
+                {
+                    KLayer &L = klayer(kargs(), l);
+                    const bf16 *wg = L.w_gate, *wu = L.w_up;
+                    pf_g.load([=](int r) { return wg + (size_t)r * H; }, g0, g1);
+                    pf_u.load([=](int r) { return wu + (size_t)r * H; }, g0, g1);
+                }
+                if constexpr (S::PF_D == PF_WITH_ATTENTION)
+                    pf_d.load(d_row(klayer(kargs(), l)), o0, o1);
+            };
+            if constexpr (SPLIT) {
+                // long histories: this workgroup's share of the split attention first; the
+                // weights after it (requested once the block statistics were out, they held the
+                // issuing waves: 4B at 8192 positions, statistics published at 16.1 us against
+                // 12.8 on the workgroups without weights; 0.6B at 4096 positions 1180 against
+                // 1418 tokens/s; requested after the o poll, the o rows then waited for them:
+                // 0.6B 1177 tokens/s)
+                KArgs &a = kargs();
+                split_attention<S>(a, klayer(a, l), opaque(pos), l, sm.split, kv, tag_of(seq),
+                                   tag_of(seq + 1), rope_c, rope_s, n_layers, step);
             }
-            if constexpr (S::PF_D == PF_WITH_ATTENTION) pf_d.load(d_row(klayer(kargs(), l)), o0, o1);
+            prefetch();
             if constexpr (S::PF_QKV == PF_WITH_ATTENTION) {
                 nq.load(klayer(kargs(), ln).attn_norm);
                 pf_qkv.load(qkv_row(klayer(kargs(), ln)), q0, q1);
@@ -1218,13 +1724,19 @@ template <int H_, int I_, int HQ_, int HKV_>
 struct Shape {
     static constexpr int H = H_, I = I_, HQ = HQ_, HKV = HKV_;
     static constexpr int NMAX = 8192;  // positions a query head attends over (LDS scores)
-    // STEP_AUTO's switch to the hipGraph step: the crossover of the two steps' per-token time,
-    // measured on MI355X (64 greedy tokens after an N(0, 1) cache of 5..8100 positions): step
-    // kernel 424 + 0.53 us per position at 0.6B, 892 + 0.52 at 1.7B, 1730 + 0.72 at 4B; hipGraph
-    // 783 + 0.024, 1120 + 0.016, 2032 + 0.02 (us per token). Measured again around the switch
-    // (kernel / graph tokens/s): 0.6B 704 1334 / 1270, 768 1226 / 1269; 1.7B 480 919 / 899, 544
-    // 879 / 896; 4B 448 516 / 499, 512 486 / 500.
-    static constexpr int SWITCH_POS = H <= 1024 ? 736 : H <= 2048 ? 512 : 480;
+    // Blocks of 64 positions of history from which attention runs split over (kv head, block)
+    // items (the split instance): the crossover of the two attention forms' per-token time,
+    // measured on MI355X (64 greedy tokens after an N(0, 1) cache; one workgroup per head /
+    // split, tokens/s): 0.6B 384 1778 / 1713, 448 1693 / 1707, 512 1480 / 1683; 1.7B 448 960 /
+    // 907, 512 888 / 905; 4B 448 517 / 504, 512 488 / 511.
+    static constexpr int SPLIT_BLOCKS = H <= 1024 ? 8 : 9;
+    // STEP_AUTO's switch to the hipGraph step (at most the kernel's longest history): where the
+    // split instance's per-token time crosses the graph's, measured on MI355X (64 greedy tokens
+    // after an N(0, 1) cache; split / graph tokens/s): 0.6B 4096 1374 / 1131, 8128 1154 / 1027
+    // (no crossover: the kernel runs every position it holds); 1.7B 4096 834 / 822, 6144 762 /
+    // 794; 4B 4096 479 / 466, 6144 440 / 448, 8192 428 / 432. The small test shape keeps a
+    // switch (736) so that a generate_greedy crossing it is exercised.
+    static constexpr int SWITCH_POS = H == 1024 ? 1 << 30 : H < 1024 ? 736 : 5120;
     // q/k/v rows per wave (one prefetched batch; 4B: 575.4-575.9 tokens/s, 1 row 544.7) and
     // where they go. A CU's vector-memory requests complete in order, so a workgroup's poll
     // lands only after every weight request it made before the poll. At 0.6B every matrix
@@ -1279,12 +1791,14 @@ using Qwen3_17B = Shape<2048, 6144, 16, 8>;
 using Qwen3_4B = Shape<2560, 9728, 32, 8>;
 using SmallTest = Shape<512, 1024, 8, 4>;
 
-static const void *step_kernel_for(const Config *c) {
+// The instance for these shapes: with `split`, the one whose attention runs split over
+// (kv head, block) items.
+static const void *step_kernel_for(const Config *c, bool split = false) {
     if (c->head_dim != 128) return nullptr;
 #define MATCH(S)                                                                            \
     if (c->hidden_size == S::H && c->intermediate_size == S::I && c->n_heads == S::HQ &&    \
         c->n_kv_heads == S::HKV)                                                           \
-        return (const void *)step_kernel<S>;
+        return split ? (const void *)step_kernel<S, true> : (const void *)step_kernel<S, false>;
     MATCH(Qwen3_06B) MATCH(Qwen3_17B) MATCH(Qwen3_4B) MATCH(SmallTest)
 #undef MATCH
     return nullptr;
@@ -1295,7 +1809,7 @@ static const void *step_kernel_for(const Config *c) {
 static bool step_grid_fits(const Config *c, int grid) {
     if (grid <= 0 || grid > 1024 || grid < 2 * c->n_heads) return false;
 #define QKV_FITS(S)                                                                         \
-    if (step_kernel_for(c) == (const void *)step_kernel<S> && qkv_first_wg<S>(grid) < S::HQ)   \
+    if (step_kernel_for(c) == (const void *)step_kernel<S, false> && qkv_first_wg<S>(grid) < S::HQ)   \
         return false;
     QKV_FITS(Qwen3_06B) QKV_FITS(Qwen3_17B) QKV_FITS(Qwen3_4B) QKV_FITS(SmallTest)
 #undef QKV_FITS
@@ -1303,13 +1817,37 @@ static bool step_grid_fits(const Config *c, int grid) {
     return rows_per_wave(c->hidden_size, (grid - c->n_heads) * WAVES) <= 64;
 }
 
-size_t step_workspace_bytes(const Config *c) {
+// The tagged vectors' words (each 4 bytes) after the StepWorkspace header.
+static size_t step_vector_words(const Config *c) {
     const size_t qd = (size_t)c->n_heads * c->head_dim, kvd = (size_t)c->n_kv_heads * c->head_dim;
-    const size_t words = STEP_REPLICAS * step_replica_stride(c->hidden_size) +
-                         step_replica_stride(qd + 2 * kvd) +
-                         STEP_REPLICAS * step_replica_stride(qd) +
-                         STEP_REPLICAS * step_replica_stride(c->intermediate_size);
-    return sizeof(StepWorkspace) + 4 * words;
+    return STEP_REPLICAS * step_replica_stride(c->hidden_size) +
+           step_replica_stride(qd + 2 * kvd) + STEP_REPLICAS * step_replica_stride(qd) +
+           STEP_REPLICAS * step_replica_stride(c->intermediate_size);
+}
+
+int step_split_max_blocks(const Config *c, int max_seq) {
+    const int mb = (max_seq + 63) / 64;
+    return mb < SPLIT_MAXB ? mb : SPLIT_MAXB;
+}
+
+// Offsets (bytes from the workspace start, 256-byte aligned) of the split attention's tagged
+// statistics and partials.
+static size_t step_stat_offset(const Config *c) {
+    return (sizeof(StepWorkspace) + 4 * step_vector_words(c) + 255) / 256 * 256;
+}
+static size_t step_part_offset(const Config *c, int max_seq) {
+    return step_stat_offset(c) + (size_t)c->n_heads * step_split_max_blocks(c, max_seq) * 2 * 8;
+}
+
+size_t step_workspace_bytes(const Config *c, int max_seq) {
+    return step_part_offset(c, max_seq) +
+           (size_t)c->n_heads * step_split_max_blocks(c, max_seq) * c->head_dim * 8;
+}
+
+void step_split_buffers(const Config *c, int max_seq, void *ws, unsigned long long **tstat,
+                        unsigned long long **tpart) {
+    *tstat = (unsigned long long *)((char *)ws + step_stat_offset(c));
+    *tpart = (unsigned long long *)((char *)ws + step_part_offset(c, max_seq));
 }
 
 bool step_kernel_available(const Config *cfg) {
@@ -1317,18 +1855,36 @@ bool step_kernel_available(const Config *cfg) {
            step_grid_fits(cfg, step_kernel_grid());
 }
 
+int step_kernel_max_seq(const Config *cfg) {
+    const int grid = step_kernel_grid();
+    if (!step_kernel_available(cfg) || (2 * grid) % cfg->n_kv_heads != 0) return 0;
+    int blocks = SPLIT_ITEMS * (2 * grid / cfg->n_kv_heads);
+    if (blocks > SPLIT_MAXB) blocks = SPLIT_MAXB;
+    return blocks * 64;
+}
+
 bool step_kernel_supported(const Config *cfg, int max_seq) {
-    return step_kernel_available(cfg) && max_seq <= 8192;
+    return step_kernel_available(cfg) && max_seq <= step_kernel_max_seq(cfg);
+}
+
+int step_kernel_split_blocks(const Config *cfg) {
+#define SPLIT(S)                                                                            \
+    if (step_kernel_for(cfg) == (const void *)step_kernel<S, false>) return S::SPLIT_BLOCKS;
+    SPLIT(Qwen3_06B) SPLIT(Qwen3_17B) SPLIT(Qwen3_4B) SPLIT(SmallTest)
+#undef SPLIT
+    return 0;
 }
 
 // Measured on MI355X, 5-token prompt then 128-256 tokens: 0.6B 2356 tokens/s (step kernel)
 // against 1278 (hipGraph), 1.7B 1121 against 893, 4B 578 against 492.
 int step_kernel_switch_pos(const Config *cfg) {
+    int sw = 0;
 #define SWITCH(S)                                                                           \
-    if (step_kernel_for(cfg) == (const void *)step_kernel<S>) return S::SWITCH_POS;
+    if (step_kernel_for(cfg) == (const void *)step_kernel<S, false>) sw = S::SWITCH_POS;
     SWITCH(Qwen3_06B) SWITCH(Qwen3_17B) SWITCH(Qwen3_4B) SWITCH(SmallTest)
 #undef SWITCH
-    return 0;
+    const int longest = step_kernel_max_seq(cfg);
+    return sw < longest ? sw : longest;
 }
 
 int step_kernel_grid() {
@@ -1349,8 +1905,9 @@ int step_kernel_grid() {
 // cooperative launch's resources ran after the profiler had shut its HSA runtime down and
 // faulted (SIGSEGV in libhsa-runtime64, called from libamdhip64's exit handler, on a
 // device-mapped page), after every result had been written.
-bool step_kernel_launch(const Config *cfg, const StepArgs &args, int grid, hipStream_t stream) {
-    const void *fn = step_kernel_for(cfg);
+bool step_kernel_launch(const Config *cfg, const StepArgs &args, bool split, int grid,
+                        hipStream_t stream) {
+    const void *fn = step_kernel_for(cfg, split);
     if (!fn) return llm_fail("step kernel: no specialisation for these shapes");
     if (!step_grid_fits(cfg, grid)) return llm_fail("step kernel: grid of %d does not fit", grid);
     int per_cu = 0, dev = 0, cus = 0;

@@ -53,7 +53,8 @@ class RunState(ctypes.Structure):
                 ("persistent", _i), ("step_ws", _vp), ("layers_dev", _vp), ("step_grid", _i),
                 ("next_token_valid", _i), ("step_trace", ctypes.POINTER(ctypes.c_longlong)),
                 ("attn_mode", _i), ("attn_one_pass_ws", _vp),
-                ("rope_table", ctypes.POINTER(ctypes.c_float)), ("step_switch_pos", _i)]
+                ("rope_table", ctypes.POINTER(ctypes.c_float)), ("step_switch_pos", _i),
+                ("step_split_blocks", _i)]
 
 
 STEP_MODES = {"auto": 0, "graph": 1, "persistent": 2}

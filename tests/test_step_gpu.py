@@ -636,6 +636,63 @@ def test_auto_step_switches_to_graph_at_switch_pos(gpu, oracle):
         dec.close()
 
 
+@pytest.mark.parametrize("split_blocks", [1, 3])
+def test_persistent_split_attention_small(gpu, oracle, split_blocks):
+    """The persistent step's split attention ((kv head, 64-position block) items over every
+    workgroup, block statistics and partials exchanged as tagged words, the partials of half a
+    head's columns added in block order by each of the last workgroups) on the smallest
+    specialised shapes (8/4 heads): with the split from the first block (split_blocks 1) and
+    from 128 positions (3), single steps at positions 0-69 and 1000-1003 after an N(0, 1) cache,
+    and a generate_greedy call of 100 tokens from 100 (which crosses the 64-position block
+    edges and, when split_blocks is 3, runs 100-127 in one launch of the per-head instance and
+    128-199 in one of the split instance): logits, argmax and tokens bit-identical to the
+    oracle."""
+    ident(f"persistent split attention small shapes, split from {split_blocks} blocks")
+    from llm_inference_amd import model
+    S = 1100
+    cfg = model.make_config(hidden_size=512, intermediate_size=1024, n_layers=3, n_heads=8,
+                            n_kv_heads=4, vocab_size=5000, max_seq_len=S)
+    dec = model.Decoder(cfg, ("synth", 8, 0.02, 0.1))
+    try:
+        rng = np.random.default_rng(split_blocks)
+        kvd = cfg.n_kv_heads * cfg.head_dim
+        k = np.zeros((cfg.n_layers, S, kvd), np.uint16)
+        v = np.zeros_like(k)
+        k[:, 200:1000] = rand_bf16(rng, (cfg.n_layers, 800, kvd))
+        v[:, 200:1000] = rand_bf16(rng, (cfg.n_layers, 800, kvd))
+        dec.set_kv_cache(k, v)
+        w = dec.host_weights()
+        orc = oracle.Model(oracle_cfg(cfg), w, max_seq=S)
+        orc.bufs["key_cache"][:] = k.reshape(-1)
+        orc.bufs["value_cache"][:] = v.reshape(-1)
+        dec.capture_graph("persistent")
+        assert dec.persistent
+        dec.s.step_split_blocks = split_blocks
+        tokens = [int(t) for t in rng.integers(0, cfg.vocab_size, 70)]
+        for pos, tok in enumerate(tokens):
+            dec.forward(tok, pos)
+            nxt = dec.sample_argmax()
+            ref = orc.forward(tok, pos, oracle.GPU_ORDER)
+            assert np.array_equal(dec.logits(), orc.logits), pos
+            assert nxt == ref, pos
+        got = dec.generate_greedy(nxt, 70, 30)
+        got += dec.generate_greedy(got[-1], 100, 100)
+        t, want = nxt, []
+        for pos in range(70, 200):
+            t = orc.forward(t, pos, oracle.GPU_ORDER)
+            want.append(t)
+        assert got == want
+        for pos in range(1000, 1004):
+            tok = int(rng.integers(0, cfg.vocab_size))
+            dec.forward(tok, pos)
+            nxt = dec.sample_argmax()
+            ref = orc.forward(tok, pos, oracle.GPU_ORDER)
+            assert np.array_equal(dec.logits(), orc.logits), pos
+            assert nxt == ref, pos
+    finally:
+        dec.close()
+
+
 @pytest.mark.parametrize("size", ["1.7B", "4B"])
 def test_persistent_step_wide_shapes(gpu, oracle, size):
     """The Qwen3-1.7B and -4B specialisations of the persistent step (their widths and heads,
@@ -702,11 +759,11 @@ def test_persistent_step_long_context(qwen06b, oracle):
 
 
 def test_persistent_step_4b_longest_history(gpu, oracle):
-    """The 4B specialisation of the persistent step (four query heads per kv head) at the longest
-    history it holds (8192 positions of scores per head in LDS): one position at 8183, then an
-    8-token generate in one launch ending at 8191, after a KV cache filled with N(0, 1) below,
-    full widths with 2 layers. Logits, argmax, the KV rows written and the generated tokens
-    bit-identical to the oracle; the next position is refused."""
+    """The 4B specialisation of the persistent step (four query heads per kv head) up to the end
+    of an 8192-position cache (split attention over 128 blocks, two items per half-slot): one
+    position at 8183, then an 8-token generate in one launch ending at 8191, after a KV cache
+    filled with N(0, 1) below, full widths with 2 layers. Logits, argmax, the KV rows written and
+    the generated tokens bit-identical to the oracle; position 8192 is refused."""
     ident("persistent step 4B widths at positions 8183..8191")
     from llm_inference_amd import LlmError, model
     S = 8192
@@ -751,16 +808,72 @@ def test_persistent_step_4b_longest_history(gpu, oracle):
         dec.close()
 
 
+def test_persistent_step_4b_after_8192_positions(gpu, oracle):
+    """The Qwen3-4B 8192-position config on the persistent step (split attention: 129-132 blocks,
+    so some half-slots hold three (kv head, block) items): full 4B widths, 2 layers, the KV
+    cache's first 8192 positions filled with N(0, 1), max_seq 8448. Logits and argmax
+    bit-identical to the oracle at 8192 and 8193, one generate_greedy launch of 8 tokens from
+    8194, and the last position 8447."""
+    ident("persistent step 4B from 8192 positions")
+    from llm_inference_amd import model
+    S = 8448
+    cfg = model.qwen3_config("4B", n_layers=2, max_seq_len=S)
+    dec = model.Decoder(cfg, ("synth", 41, 0.02, 0.1))
+    try:
+        rng = np.random.default_rng(8448)
+        kvd = cfg.n_kv_heads * cfg.head_dim
+        k = np.zeros((cfg.n_layers, S, kvd), np.uint16)
+        v = np.zeros_like(k)
+        k[:, :8192] = rand_bf16(rng, (cfg.n_layers, 8192, kvd))
+        v[:, :8192] = rand_bf16(rng, (cfg.n_layers, 8192, kvd))
+        k[:, 8202:] = rand_bf16(rng, (cfg.n_layers, S - 8202, kvd))
+        v[:, 8202:] = rand_bf16(rng, (cfg.n_layers, S - 8202, kvd))
+        dec.set_kv_cache(k, v)
+        w = dec.host_weights()
+        orc = oracle.Model(oracle_cfg(cfg), w, max_seq=S)
+        del w
+        orc.bufs["key_cache"][:] = k.reshape(-1)
+        orc.bufs["value_cache"][:] = v.reshape(-1)
+        dec.capture_graph("persistent")
+        assert dec.persistent
+        tok = int(rng.integers(0, cfg.vocab_size))
+        for pos in (8192, 8193):
+            dec.forward(tok, pos)
+            nxt = dec.sample_argmax()
+            ref = orc.forward(tok, pos, oracle.GPU_ORDER)
+            assert np.array_equal(dec.logits(), orc.logits), pos
+            assert nxt == ref, pos
+            tok = nxt
+        got = dec.generate_greedy(tok, 8194, 8)
+        want = []
+        for i in range(8):
+            tok = orc.forward(tok, 8194 + i, oracle.GPU_ORDER)
+            want.append(tok)
+        assert got == want
+        kk, vv = dec.kv_cache()
+        ok = orc.bufs["key_cache"].reshape(k.shape)
+        ov = orc.bufs["value_cache"].reshape(v.shape)
+        assert np.array_equal(kk[:, 8192:8202], ok[:, 8192:8202])
+        assert np.array_equal(vv[:, 8192:8202], ov[:, 8192:8202])
+        dec.forward(99, 8447)
+        nxt = dec.sample_argmax()
+        ref = orc.forward(99, 8447, oracle.GPU_ORDER)
+        assert np.array_equal(dec.logits(), orc.logits)
+        assert nxt == ref
+    finally:
+        dec.close()
+
+
 @pytest.mark.parametrize("size", ["1.7B", "4B"])
 def test_persistent_step_wide_shapes_long_history(gpu, oracle, size):
     """The 1.7B and 4B specialisations of the persistent step (2 and 4 query heads per kv head)
-    where the bench and STEP_AUTO run them: single positions 260 (five 64-position blocks) and
-    the last position before STEP_AUTO's switch to the hipGraph (511 at 1.7B, 479 at 4B: eight
-    blocks) after a KV cache filled with N(0, 1) below them, at full widths with 2 layers.
-    Logits, argmax and the KV rows written bit-identical to the oracle; then an 8-token generate
-    that ends at that position, in one launch."""
-    last = {"1.7B": 511, "4B": 479}[size]
-    ident(f"persistent step {size} widths at positions 260 and {last}")
+    around their switch from one workgroup per query head to the split attention (from 512
+    positions): single positions 260 and 511 (per head) and 512 (split) after a KV cache filled
+    with N(0, 1) below them, at full widths with 2 layers; logits, argmax and the KV rows
+    written bit-identical to the oracle. Then one generate_greedy call of 16 tokens from 505,
+    which runs 505-511 in one launch of the per-head instance and 512-520 in one of the split
+    instance, continuing from the token and position the first left."""
+    ident(f"persistent step {size} widths at positions 260, 511, 512")
     from llm_inference_amd import model
     S = 528
     cfg = model.qwen3_config(size, n_layers=2, max_seq_len=S)
@@ -777,10 +890,10 @@ def test_persistent_step_wide_shapes_long_history(gpu, oracle, size):
         orc.bufs["key_cache"][:] = k.reshape(-1)
         orc.bufs["value_cache"][:] = v.reshape(-1)
         dec.capture_graph("auto")
-        assert dec.s.step_switch_pos == last + 1
+        assert dec.s.step_split_blocks == 9 and dec.s.step_switch_pos == S
         dec.capture_graph("persistent")
         assert dec.persistent
-        for pos in (260, last):
+        for pos in (260, 511, 512):
             tok = int(rng.integers(0, cfg.vocab_size))
             dec.forward(tok, pos)
             nxt = dec.sample_argmax()
@@ -792,10 +905,10 @@ def test_persistent_step_wide_shapes_long_history(gpu, oracle, size):
             ov = orc.bufs["value_cache"].reshape(v.shape)
             assert np.array_equal(kk[:, pos], ok[:, pos]), pos
             assert np.array_equal(vv[:, pos], ov[:, pos]), pos
-        got = dec.generate_greedy(nxt, last - 7, 8)
+        got = dec.generate_greedy(nxt, 505, 16)
         t, want = nxt, []
-        for i in range(8):
-            t = orc.forward(t, last - 7 + i, oracle.GPU_ORDER)
+        for i in range(16):
+            t = orc.forward(t, 505 + i, oracle.GPU_ORDER)
             want.append(t)
         assert got == want
     finally:

@@ -62,14 +62,17 @@ def test_step_kernels_have_no_calls_and_no_flat_access(step_asm):
 
 
 def test_bench_shape_step_kernel_uses_no_scratch(step_asm):
-    """The Qwen3-0.6B instance (the bench's) and the small test shape keep everything in
-    registers and LDS: no spill and no private array (a local table indexed at run time is placed
-    in scratch memory, whose loads cost a memory round trip)."""
+    """The Qwen3-0.6B instance with one workgroup per query head (the bench's) and the small test
+    shape's keep everything in registers and LDS: no spill and no private array (a local table
+    indexed at run time is placed in scratch memory, whose loads cost a memory round trip). The
+    0.6B split-attention instance is allowed a few bytes, reloaded once per token."""
     sizes = dict(re.findall(r"\.name:\s+(\S+)\n(?:.*\n)*?\s+\.private_segment_fixed_size:\s+(\d+)",
                             step_asm))
     checked = 0
     for name, size in sizes.items():
-        if "ShapeILi1024ELi3072ELi16ELi8E" in name or "ShapeILi512ELi1024ELi8ELi4E" in name:
+        if "ShapeILi1024ELi3072ELi16ELi8EELb0E" in name or "ShapeILi512ELi1024ELi8ELi4EELb0E" in name:
             assert int(size) == 0, (name, size)
             checked += 1
+        elif "ShapeILi1024ELi3072ELi16ELi8EELb1E" in name:
+            assert int(size) <= 32, (name, size)
     assert checked == 2, sizes
