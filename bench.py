@@ -725,15 +725,15 @@ def config_decoder(size, n_prefill, steps):
     return dec, first, start, prompt, k, v
 
 
-def decode_config(size, n_prefill, steps, cpu_budget_s, read_peak=None, compare_graph=False):
+def decode_config(size, n_prefill, steps, cpu_budget_s, read_peak=None, compare=None):
     """Greedy decode tokens/s of one more model config at batch 1: Qwen3-`size` shapes with the
     bench's seeded weights, either after a 5-token prompt or (n_prefill > 0) after a KV cache
     whose first n_prefill positions hold N(0, 1) keys and values (bf16 by truncation). `steps`
     tokens per generate call, the median of RUNS calls after a warm-up; the step is STEP_AUTO's
     (the persistent kernel below its switch position, the hipGraph of per-layer kernels from
     there on). With cpu_budget_s, the oracle decodes the same model from the same state for
-    about that long; with compare_graph, the hipGraph step decodes the same tokens too (its
-    tokens/s beside the line's)."""
+    about that long; with compare ("graph" or "persistent"), that step decodes the same tokens
+    too (its tokens/s beside the line's)."""
     dec, first, start, prompt, k, v = config_decoder(size, n_prefill, steps)
     max_seq = dec.s.max_seq
     dt, _, walls, tokens = timed_runs(dec, first, start, steps, 8)
@@ -750,13 +750,14 @@ def decode_config(size, n_prefill, steps, cpu_budget_s, read_peak=None, compare_
            "first_tokens": tokens[:4]}
     log(f"Qwen3-{size}: {out['tokens_per_s']} tokens/s ({out['step']}), "
         f"{out['effective_GB/s']} GB/s")
-    if compare_graph:
-        dec.capture_graph("graph")
-        gdt, _, _, gtokens = timed_runs(dec, first, start, steps, 8)
-        if gtokens != tokens:
-            raise RuntimeError("bench: the hipGraph step decoded other tokens")
-        out["graph_tokens_per_s"] = round(steps / gdt, 2)
-        log(f"  the same on the hipGraph step: {out['graph_tokens_per_s']} tokens/s")
+    if compare:
+        dec.capture_graph(compare)
+        cdt, _, _, ctokens = timed_runs(dec, first, start, steps, 8)
+        if ctokens != tokens:
+            raise RuntimeError(f"bench: the {compare} step decoded other tokens")
+        out[f"{compare}_tokens_per_s"] = round(steps / cdt, 2)
+        out[f"{compare}_step"] = dec.step_kind(start, steps)
+        log(f"  the same on the {out[f'{compare}_step']}: {out[f'{compare}_tokens_per_s']} tokens/s")
     if cpu_budget_s:
         sys.path.insert(0, str(ROOT / "oracle"))
         import oracle
@@ -862,7 +863,9 @@ def run_bench(args):
     # untimed, then exactly --steps steps inside one timed region bracketed by device syncs;
     # HIP events on the step's stream time each step's device work.
     k_tok = dec.kernel_tokens(n_prompt, n_gen)
-    launches = (1 if k_tok else 0) + n_gen - k_tok  # per step
+    split_from = (dec.s.step_split_blocks - 1) * 64  # the kernel's split attention from here
+    kernel_launches = 0 if not k_tok else 2 if n_prompt < split_from < n_prompt + k_tok else 1
+    launches = kernel_launches + n_gen - k_tok  # per step
     for _ in range(args.warmup):
         dec.generate_greedy(first, n_prompt, n_gen)
     stream = torch.cuda.ExternalStream(dec.stream)
@@ -982,16 +985,18 @@ def run_bench(args):
     dec.close()
     if not args.no_configs:
         # the other decode configs of the metric: Qwen3-1.7B and Qwen3-4B after a 5-token prompt,
-        # and Qwen3-4B after an 8192-position cache (mean position 8320.5), 256 tokens each; and
-        # Qwen3-0.6B after an 8192-position cache, where the step kernel's split attention runs
-        # (beside the hipGraph step on the same tokens)
+        # and Qwen3-4B after an 8192-position cache (mean position 8320.5), 256 tokens each
+        # (beside the persistent kernel's split attention on the same tokens); and Qwen3-0.6B
+        # after an 8192-position cache, where the kernel's split attention runs (beside the
+        # hipGraph step on the same tokens)
         budget = 0 if args.no_cpu_baseline else 10.0
         line["decode_configs"] = {
             "qwen3_1.7B": decode_config("1.7B", 0, 256, budget, read_peak),
             "qwen3_4B": decode_config("4B", 0, 256, None, read_peak),
-            "qwen3_4B_ctx8192": decode_config("4B", 8192, 256, budget, read_peak),
+            "qwen3_4B_ctx8192": decode_config("4B", 8192, 256, budget, read_peak,
+                                              compare="persistent"),
             "qwen3_0.6B_ctx8192": decode_config("0.6B", 8192, 256, None, read_peak,
-                                                compare_graph=True),
+                                                compare="graph"),
         }
         line["fused_layer_4B"] = fused_layer_rate("4B", read_peak)
     print(json.dumps(line), flush=True)

@@ -868,6 +868,28 @@ __device__ __forceinline__ void split_request(KArgs &a, int pos, int pos0, int l
         }
 }
 
+// scatter_keep<M, 16, 64> (the position groups' reduce-scatter of pv_item) with
+// v_permlane16_swap and v_permlane32_swap: swapping the rows of values j and j + M/2 pairs each
+// lane with its xor-16 (then xor-32) partner as the butterfly does, and leaves in each lane the
+// half it keeps, so the sums (a + b = b + a) and the kept values are those of scatter_keep
+// without its per-lane selects.
+template <int M>
+__device__ __forceinline__ void scatter_keep_swap(const float (&v)[M], float (&out)[M / 4]) {
+    float k1[M / 2];
+#pragma unroll
+    for (int j = 0; j < M / 2; j++) {
+        const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[j]),
+                                                        __float_as_uint(v[j + M / 2]), false, false);
+        k1[j] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+#pragma unroll
+    for (int j = 0; j < M / 4; j++) {
+        const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(k1[j]),
+                                                        __float_as_uint(k1[j + M / 4]), false, false);
+        out[j] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+}
+
 __device__ __forceinline__ void put_tagged64(unsigned long long *p, float v, uint32_t tag) {
     __hip_atomic_store(gptr(p), ((unsigned long long)__float_as_uint(v) << 32) | tag,
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -902,7 +924,7 @@ __device__ __forceinline__ void poll_tagged64(int t, int count, uint32_t tag, in
 // entry at pos.
 template <class S>
 __device__ __forceinline__ void split_attention(KArgs &a, KLayer &L, int pos, int layer,
-                                                SplitSmem<S> &sm, const SplitKV &kv,
+                                                SplitSmem<S> &sm, SplitKV &kv,
                                                 uint32_t tag_in, uint32_t tag_out, float cs,
                                                 float sn, int n_layers, int step) {
     constexpr int D = 128, REP = S::HQ / S::HKV, QD = S::HQ * D, KVD = S::HKV * D;
@@ -983,6 +1005,22 @@ __device__ __forceinline__ void split_attention(KArgs &a, KLayer &L, int pos, in
             st_kv(vc + row + 64 + lane, v16[64 + lane]);
         }
         __syncthreads();
+        // the item holding pos takes its key and value (row pos of the caches, just written)
+        // into the slot of pos, once, instead of a select in every slot of every item
+        if (has_pos) {
+            const u32x4 kcur = sm.k[hf][Lk];
+            const u32x4 vcur = ((const u32x4 *)sm.raw[hf][REP + 1])[Lk];
+#pragma unroll
+            for (int k = 0; k < SPLIT_ITEMS; k++)
+                if (j0 + k * spg == pb) {
+#pragma unroll
+                    for (int it = 0; it < 4; it++) {
+                        const bool at = pb * 64 + w4 * 16 + it * 4 + G == pos;
+                        kv.k[k][it] = at ? kcur : kv.k[k][it];
+                        kv.v[k][it] = at ? vcur : kv.v[k][it];
+                    }
+                }
+        }
         // scores s = bf16(bf16(q.k) * scale) of each item (attn_scores_kernel layout: slot
         // w4 * 16 + it * 4 + G, 16 lanes per position, reduce-scattered)
         {
@@ -996,7 +1034,6 @@ __device__ __forceinline__ void split_attention(KArgs &a, KLayer &L, int pos, in
 #pragma unroll
                 for (int e = 0; e < 8; e++) qf[r][e] = elem(qv, e);
             }
-            const u32x4 kcur = sm.k[hf][Lk];
 #pragma unroll
             for (int k = 0; k < SPLIT_ITEMS; k++) {
                 const int b = j0 + k * spg;
@@ -1005,8 +1042,7 @@ __device__ __forceinline__ void split_attention(KArgs &a, KLayer &L, int pos, in
                 float part[NP];
 #pragma unroll
                 for (int it = 0; it < 4; it++) {
-                    const int t = b * 64 + w4 * 16 + it * 4 + G;
-                    const u32x4 kt = t == pos ? kcur : kv.k[k][it];
+                    const u32x4 kt = kv.k[k][it];
                     float kf[8];
 #pragma unroll
                     for (int e = 0; e < 8; e++) kf[e] = elem(kt, e);
@@ -1108,7 +1144,6 @@ __device__ __forceinline__ void split_attention(KArgs &a, KLayer &L, int pos, in
         // PV of each item (pv_item layout: per lane over its slots in order, the position
         // groups reduce-scattered with the butterfly's pairing, the four waves added in order),
         // published per head and element
-        const u32x4 vcur = ((const u32x4 *)sm.raw[hf][REP + 1])[Lk];
         // the KV row this workgroup may have stored is complete before any partial that later
         // steps depend on is published
         __builtin_amdgcn_s_waitcnt(0);
@@ -1127,7 +1162,7 @@ __device__ __forceinline__ void split_attention(KArgs &a, KLayer &L, int pos, in
                     const int slot = w4 * 16 + it * 4 + G;
                     const int t = b * 64 + slot;
                     if (t < n) {
-                        const u32x4 vt = t == pos ? vcur : kv.v[k][it];
+                        const u32x4 vt = kv.v[k][it];
 #pragma unroll
                         for (int r = 0; r < REP; r++) {
                             const float p = sm.sc[hf][k][r][slot];
@@ -1142,7 +1177,7 @@ __device__ __forceinline__ void split_attention(KArgs &a, KLayer &L, int pos, in
                 for (int r = 0; r < REP; r++)
 #pragma unroll
                     for (int e = 0; e < 8; e++) flat[r * 8 + e] = acc[r][e];
-                scatter_keep<NV, 16, 64>(flat, kept);
+                scatter_keep_swap<NV>(flat, kept);
                 int off = 0;
 #pragma unroll
                 for (int q = 0, m = NV; (16 << q) < 64; q++, m >>= 1)
@@ -1167,7 +1202,7 @@ __device__ __forceinline__ void split_attention(KArgs &a, KLayer &L, int pos, in
         }
     }
     // the last 2 HQ workgroups: columns [c0, c0 + COMB_COLS) of query head h, out = bf16(block
-    // partials added in block order), every block's partials polled at once
+    // partials added in block order)
     const int task = (int)blockIdx.x - ((int)gridDim.x - S::HQ * (D / COMB_COLS));
     if (task >= 0) {
         const int h = task / (D / COMB_COLS), c0 = (task % (D / COMB_COLS)) * COMB_COLS;
@@ -1181,8 +1216,10 @@ __device__ __forceinline__ void split_attention(KArgs &a, KLayer &L, int pos, in
         const int voff = (tb * D + tc) * 8;
         __syncthreads();
         // first the column-c0 word of every block (one per thread; an item stores all its words
-        // at once): re-reading every partial while most are still being written would stream
-        // the whole set once per poll round
+        // at once), then every partial in one read: re-reading all of them while most are still
+        // being written streams the whole set once per poll round (4B at 8192 positions: 409
+        // tokens/s with two threads per block polling its 32 words each; 427 with eight
+        // threads per block in passes of 64 blocks; 438 as here)
         if ((int)threadIdx.x < nb) {
             const unsigned long long *w0 = a.tpart + ((size_t)h * mb + threadIdx.x) * D + c0;
             long long spins = 0;
@@ -1486,30 +1523,27 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
             Rows<NCH, S::B_GU> pf_g{}, pf_u{};
             Rows<NCI, S::B_DOWN> pf_d{};
             NormW<H> ng{};  // mlp_norm weights
-            auto prefetch = [&]() __attribute__((always_inline)) {
-                pf_o.load(o_row(klayer(kargs(), l)), o0, o1);
-                ng.load(klayer(kargs(), l).mlp_norm);
-                {
-                    KLayer &L = klayer(kargs(), l);
-                    const bf16 *wg = L.w_gate, *wu = L.w_up;
-                    pf_g.load([=](int r) { return wg + (size_t)r * H; }, g0, g1);
-                    pf_u.load([=](int r) { return wu + (size_t)r * H; }, g0, g1);
-                }
-                if constexpr (S::PF_D == PF_WITH_ATTENTION)
-                    pf_d.load(d_row(klayer(kargs(), l)), o0, o1);
-            };
             if constexpr (SPLIT) {
                 // long histories: this workgroup's share of the split attention first; the
                 // weights after it (requested once the block statistics were out, they held the
                 // issuing waves: 4B at 8192 positions, statistics published at 16.1 us against
                 // 12.8 on the workgroups without weights; 0.6B at 4096 positions 1180 against
                 // 1418 tokens/s; requested after the o poll, the o rows then waited for them:
-                // 0.6B 1177 tokens/s)
+                // 0.6B 1177 tokens/s; the gate/up rows alone after the o poll: 0.6B 1299, 4B at
+                // 8192 positions 419 against 428)
                 KArgs &a = kargs();
                 split_attention<S>(a, klayer(a, l), opaque(pos), l, sm.split, kv, tag_of(seq),
                                    tag_of(seq + 1), rope_c, rope_s, n_layers, step);
             }
-            prefetch();
+            pf_o.load(o_row(klayer(kargs(), l)), o0, o1);
+            ng.load(klayer(kargs(), l).mlp_norm);
+            {
+                KLayer &L = klayer(kargs(), l);
+                const bf16 *wg = L.w_gate, *wu = L.w_up;
+                pf_g.load([=](int r) { return wg + (size_t)r * H; }, g0, g1);
+                pf_u.load([=](int r) { return wu + (size_t)r * H; }, g0, g1);
+            }
+            if constexpr (S::PF_D == PF_WITH_ATTENTION) pf_d.load(d_row(klayer(kargs(), l)), o0, o1);
             if constexpr (S::PF_QKV == PF_WITH_ATTENTION) {
                 nq.load(klayer(kargs(), ln).attn_norm);
                 pf_qkv.load(qkv_row(klayer(kargs(), ln)), q0, q1);
@@ -1518,6 +1552,7 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
             if (wg_o)
                 stage_vector<QD, OW>(my_copy<QD, S::REPLICAS>(kargs().tattn), tag_of(seq + 1), sm.vec,
                                      kargs().error_flag);
+
             stamp<S>(2 + 4 * l, step);
             stamp_wg(l, n_layers, 2, step);
             if constexpr (S::PF_D == PF_AFTER_POLL) pf_d.load(d_row(klayer(kargs(), l)), o0, o1);

@@ -249,11 +249,18 @@ class Decoder:
         return max(0, min(n, self.s.step_switch_pos - pos))
 
     def step_kind(self, pos, n):
+        """Which step decodes n tokens from `pos`: the persistent kernel (its attention one
+        workgroup per query head, or split over (kv head, block) items from
+        `s.step_split_blocks` blocks of history on) and/or the hipGraph."""
         k = self.kernel_tokens(pos, n)
-        if k == n:
-            return "persistent step kernel"
-        return "hipGraph of per-layer kernels" if k == 0 else \
-            f"persistent step kernel ({k} tokens), then hipGraph of per-layer kernels"
+        if k == 0:
+            return "hipGraph of per-layer kernels"
+        split_from = (self.s.step_split_blocks - 1) * 64
+        heads = 0 if pos >= split_from else min(k, split_from - pos)
+        form = ("one workgroup per query head" if heads == k else "split attention" if heads == 0
+                else f"one workgroup per query head for {heads} tokens, then split attention")
+        kind = f"persistent step kernel, {form}"
+        return kind if k == n else f"{kind}, for {k} tokens, then hipGraph of per-layer kernels"
 
     def forward(self, token, pos):
         lib().forward(ctypes.byref(self.cfg), ctypes.byref(self.w), ctypes.byref(self.s), token,
