@@ -798,13 +798,13 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
 // head; the host checks that the history fits). An item publishes its query heads' block
 // statistics (max, sum of exp(s - max)) and, once every block's statistics of its kv head are
 // in, its heads' block partials of p v, as tagged 64-bit words (float bits << 32 | tag); the
-// last 2 HQ workgroups of the grid (which own no o rows) then each add the partials of half a
-// head's columns in block order and publish them. Every workgroup takes part: its items' key
+// attention workgroups and the last workgroups of the grid then each add the partials of a
+// quarter of a head's columns in block order and publish them. Every workgroup takes part: its items' key
 // and value rows are requested before it polls the q/k/v vector, so the history streams on
 // every CU at once.
 constexpr int SPLIT_ITEMS = 3;   // items of a half-slot at most
 constexpr int SPLIT_MAXB = 192;  // blocks of 64 positions at most (3 chunks of 64 statistics)
-constexpr int COMB_COLS = 64;    // columns of a head one workgroup combines
+constexpr int COMB_COLS = 32;    // columns of a head one workgroup combines
 
 template <class S>
 struct SplitSmem {
@@ -1201,9 +1201,14 @@ __device__ __forceinline__ void split_attention(KArgs &a, KLayer &L, int pos, in
             __syncthreads();  // red is rewritten by the next item
         }
     }
-    // the last 2 HQ workgroups: columns [c0, c0 + COMB_COLS) of query head h, out = bf16(block
-    // partials added in block order)
-    const int task = (int)blockIdx.x - ((int)gridDim.x - S::HQ * (D / COMB_COLS));
+    // NT = HQ D / COMB_COLS combining tasks: columns [c0, c0 + COMB_COLS) of query head h, out =
+    // bf16(block partials added in block order). Tasks 0..HQ-1 run on the attention
+    // workgroups, the others on the last workgroups of the grid: workgroups that own no o rows,
+    // whose weight requests (made after this) the o phase would wait for.
+    constexpr int NT = S::HQ * (D / COMB_COLS);
+    const int tail0 = (int)gridDim.x - (NT - S::HQ);
+    const int task = (int)blockIdx.x < S::HQ ? (int)blockIdx.x
+                     : (int)blockIdx.x >= tail0 ? S::HQ + (int)blockIdx.x - tail0 : -1;
     if (task >= 0) {
         const int h = task / (D / COMB_COLS), c0 = (task % (D / COMB_COLS)) * COMB_COLS;
         // thread t reads column t % 64 of blocks t / 64 + 8 j, as buffer loads with one lane
@@ -1842,7 +1847,11 @@ static const void *step_kernel_for(const Config *c, bool split = false) {
 // The kernel's layout needs workgroups beyond the attention ones (at least as many again) and
 // at most 64 residual rows per matrix wave (7 matrix waves per workgroup when wave 0 polls).
 static bool step_grid_fits(const Config *c, int grid) {
-    if (grid <= 0 || grid > 1024 || grid < 2 * c->n_heads) return false;
+    // (the split attention's combining workgroups, D / COMB_COLS per query head, are the last
+    // ones of the grid)
+    if (grid <= 0 || grid > 1024 || grid < 2 * c->n_heads ||
+        grid < (128 / COMB_COLS) * c->n_heads)
+        return false;
 #define QKV_FITS(S)                                                                         \
     if (step_kernel_for(c) == (const void *)step_kernel<S, false> && qkv_first_wg<S>(grid) < S::HQ)   \
         return false;
