@@ -812,6 +812,9 @@ def main():
     ap.add_argument("--config4-workload", action="store_true",
                     help="only run 8 greedy tokens of Qwen3-4B after an 8192-position cache "
                          "(hipGraph step), then the counter-calibrating copies")
+    ap.add_argument("--decode-config", choices=list(DECODE_CONFIGS),
+                    help="only run one of the decode lines beside the headline (256 greedy "
+                         "tokens; no CPU baseline) and print its JSON")
     ap.add_argument("--phase-trace", nargs="?", const="0.6B", choices=["0.6B", "1.7B", "4B"],
                     help="only print where a Qwen3 layer's time goes in the step kernel (the "
                          "kernel's own per-phase wall-clock stamps; default size 0.6B)")
@@ -832,10 +835,30 @@ def main():
         config4_workload()
     elif args.phase_trace:
         print(json.dumps(phase_trace(size=args.phase_trace)), flush=True)
+    elif args.decode_config:
+        load_package()
+        print(json.dumps({args.decode_config: run_decode_config(args.decode_config, 0)}),
+              flush=True)
     else:
         run_bench(args)
     if args.maps_out:
         Path(args.maps_out).write_text(Path("/proc/self/maps").read_text())
+
+
+# The decode lines beside the headline: (size, prefilled positions, whether the CPU oracle runs
+# too, the other step decoding the same tokens).
+DECODE_CONFIGS = {
+    "qwen3_1.7B": ("1.7B", 0, True, None),
+    "qwen3_4B": ("4B", 0, False, None),
+    "qwen3_4B_ctx8192": ("4B", 8192, True, "persistent"),
+    "qwen3_0.6B_ctx8192": ("0.6B", 8192, False, "graph"),
+}
+
+
+def run_decode_config(name, cpu_budget_s, read_peak=None):
+    size, n_prefill, cpu, compare = DECODE_CONFIGS[name]
+    return decode_config(size, n_prefill, 256, cpu_budget_s if cpu else None, read_peak,
+                         compare=compare)
 
 
 def run_bench(args):
@@ -990,14 +1013,8 @@ def run_bench(args):
         # after an 8192-position cache, where the kernel's split attention runs (beside the
         # hipGraph step on the same tokens)
         budget = 0 if args.no_cpu_baseline else 10.0
-        line["decode_configs"] = {
-            "qwen3_1.7B": decode_config("1.7B", 0, 256, budget, read_peak),
-            "qwen3_4B": decode_config("4B", 0, 256, None, read_peak),
-            "qwen3_4B_ctx8192": decode_config("4B", 8192, 256, budget, read_peak,
-                                              compare="persistent"),
-            "qwen3_0.6B_ctx8192": decode_config("0.6B", 8192, 256, None, read_peak,
-                                                compare="graph"),
-        }
+        line["decode_configs"] = {name: run_decode_config(name, budget, read_peak)
+                                  for name in DECODE_CONFIGS}
         line["fused_layer_4B"] = fused_layer_rate("4B", read_peak)
     print(json.dumps(line), flush=True)
 

@@ -864,6 +864,60 @@ def test_persistent_step_4b_after_8192_positions(gpu, oracle):
         dec.close()
 
 
+def test_persistent_split_attention_longest_history(gpu, oracle):
+    """The split attention at the longest history the persistent kernel holds: 192 blocks of 64
+    positions (three items on half of the half-slots at Qwen3-0.6B's 8 kv heads on 256 CUs, the
+    combine over every block the workspace holds), full 0.6B widths with 2 layers after an
+    N(0, 1) cache. Position 12286 alone, then a generate of the last position, bit-identical to
+    the oracle; a run state one position longer has no persistent step."""
+    ident("persistent split attention at the longest history")
+    from llm_inference_amd import LlmError, model
+    probe = model.Decoder(model.qwen3_config("0.6B", n_layers=1, max_seq_len=64),
+                          ("synth", 1, 0.02, 0.1))
+    try:
+        probe.capture_graph("persistent")
+        grid = probe.s.step_grid
+    finally:
+        probe.close()
+    S = min(192, 3 * (2 * grid // 8)) * 64
+    cfg = model.qwen3_config("0.6B", n_layers=2, max_seq_len=S)
+    dec = model.Decoder(cfg, ("synth", 43, 0.02, 0.1))
+    try:
+        rng = np.random.default_rng(S)
+        kvd = cfg.n_kv_heads * cfg.head_dim
+        k = rand_bf16(rng, (cfg.n_layers, S, kvd))
+        v = rand_bf16(rng, (cfg.n_layers, S, kvd))
+        dec.set_kv_cache(k, v)
+        w = dec.host_weights()
+        orc = oracle.Model(oracle_cfg(cfg), w, max_seq=S)
+        del w
+        orc.bufs["key_cache"][:] = k.reshape(-1)
+        orc.bufs["value_cache"][:] = v.reshape(-1)
+        dec.capture_graph("auto")
+        assert dec.persistent and dec.s.step_switch_pos == S  # 0.6B: the kernel throughout
+        tok = int(rng.integers(0, cfg.vocab_size))
+        dec.forward(tok, S - 2)
+        nxt = dec.sample_argmax()
+        ref = orc.forward(tok, S - 2, oracle.GPU_ORDER)
+        assert np.array_equal(dec.logits(), orc.logits)
+        assert nxt == ref
+        got = dec.generate_greedy(nxt, S - 1, 1)
+        assert got == [orc.forward(nxt, S - 1, oracle.GPU_ORDER)]
+        assert np.array_equal(dec.logits(), orc.logits)
+        kk, vv = dec.kv_cache()
+        assert np.array_equal(kk[:, S - 2:], orc.bufs["key_cache"].reshape(k.shape)[:, S - 2:])
+        assert np.array_equal(vv[:, S - 2:], orc.bufs["value_cache"].reshape(v.shape)[:, S - 2:])
+    finally:
+        dec.close()
+    longer = model.Decoder(model.qwen3_config("0.6B", n_layers=1, max_seq_len=S + 1),
+                           ("synth", 1, 0.02, 0.1))
+    try:
+        with pytest.raises(LlmError, match="no persistent step kernel"):
+            longer.capture_graph("persistent")
+    finally:
+        longer.close()
+
+
 @pytest.mark.parametrize("size", ["1.7B", "4B"])
 def test_persistent_step_wide_shapes_long_history(gpu, oracle, size):
     """The 1.7B and 4B specialisations of the persistent step (2 and 4 query heads per kv head)
