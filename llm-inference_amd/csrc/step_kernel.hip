@@ -793,13 +793,13 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
 // Long histories: attention split over (kv head g, 64-position block b) items, each run by half
 // a workgroup (waves 4h..4h+3, 256 threads) with the lane layout and arithmetic of the
 // multi-kernel step's passes (attn_scores_kernel, pv_item, the block-order combine), so the
-// results are those of that step bit for bit. Half-slot s = 2 * workgroup + h takes kv head
-// s % HKV and blocks s / HKV + k * SPG, k < SPLIT_ITEMS (SPG = 2 * grid / HKV half-slots per kv
-// head; the host checks that the history fits). An item publishes its query heads' block
-// statistics (max, sum of exp(s - max)) and, once every block's statistics of its kv head are
-// in, its heads' block partials of p v, as tagged 64-bit words (float bits << 32 | tag); the
-// attention workgroups and the last workgroups of the grid then each add the partials of a
-// quarter of a head's columns in block order and publish them. Every workgroup takes part: its items' key
+// results are those of that step bit for bit. Half-slot s (split_items) takes kv head s % HKV
+// and blocks s / HKV + k * SPG, k < SPLIT_ITEMS (SPG = 2 * grid / HKV half-slots per kv head;
+// the host checks that the history fits). An item publishes its query heads' block statistics
+// (max, sum of exp(s - max)) and, once every block's statistics of its kv head are in, its
+// heads' block partials of p v, as tagged 64-bit words (float bits << 32 | tag); the attention
+// workgroups and the last workgroups of the grid then each add the partials of a quarter of a
+// head's columns in block order and publish them. Every workgroup takes part: its items' key
 // and value rows are requested before it polls the q/k/v vector, so the history streams on
 // every CU at once.
 constexpr int SPLIT_ITEMS = 3;   // items of a half-slot at most
@@ -878,14 +878,14 @@ __device__ __forceinline__ void scatter_keep_swap(const float (&v)[M], float (&o
     float k1[M / 2];
 #pragma unroll
     for (int j = 0; j < M / 2; j++) {
-        const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[j]),
-                                                        __float_as_uint(v[j + M / 2]), false, false);
+        const auto p = __builtin_amdgcn_permlane16_swap(
+            __float_as_uint(v[j]), __float_as_uint(v[j + M / 2]), false, false);
         k1[j] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
     }
 #pragma unroll
     for (int j = 0; j < M / 4; j++) {
-        const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(k1[j]),
-                                                        __float_as_uint(k1[j + M / 4]), false, false);
+        const auto p = __builtin_amdgcn_permlane32_swap(
+            __float_as_uint(k1[j]), __float_as_uint(k1[j + M / 4]), false, false);
         out[j] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
     }
 }
@@ -893,29 +893,6 @@ __device__ __forceinline__ void scatter_keep_swap(const float (&v)[M], float (&o
 __device__ __forceinline__ void put_tagged64(unsigned long long *p, float v, uint32_t tag) {
     __hip_atomic_store(gptr(p), ((unsigned long long)__float_as_uint(v) << 32) | tag,
                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Polls the tagged 64-bit words src(i), i < count (count >= 1), thread t taking i = t + T j
-// (j < P), until every tag is `tag`, then hands each value to dst(i, v). Lanes past the count
-// re-read the last word, so no branch surrounds a load. Bounded as stage_pairs.
-template <int P, int T, class Src, class Dst>
-__device__ __forceinline__ void poll_tagged64(int t, int count, uint32_t tag, int *err, Src src,
-                                              Dst dst) {
-    uint64_t w[P];
-    long long spins = 0;
-    for (;;) {
-        bool fresh = true;
-#pragma unroll
-        for (int j = 0; j < P; j++) {
-            w[j] = ld_coh64(src(min(t + T * j, count - 1)));
-            fresh &= (uint32_t)w[j] == tag;
-        }
-        if (fresh) break;
-        if ((++spins & 63) == 0 && wait_gives_up(spins, SPIN_LIMIT, err)) break;
-    }
-#pragma unroll
-    for (int j = 0; j < P; j++)
-        if (t + T * j < count) dst(t + T * j, __uint_as_float((uint32_t)(w[j] >> 32)));
 }
 
 // The split attention of layer `layer` at `pos` (n = pos + 1 > 0 positions, at most
@@ -1061,7 +1038,8 @@ __device__ __forceinline__ void split_attention(KArgs &a, KLayer &L, int pos, in
                     for (int j = 0; j < SL; j++) slice[j] = part[s0 + j];
                     const float d = group_sum_scatter<16, SL>(slice);
                     const int j = s0 + scatter_row<SL>(Lk), it = j / REP, r = j - it * REP;
-                    if (Lk < SL) sm.sc[hf][k][r][w4 * 16 + it * 4 + G] = round_bf(round_bf(d) * a.scale);
+                    if (Lk < SL)
+                        sm.sc[hf][k][r][w4 * 16 + it * 4 + G] = round_bf(round_bf(d) * a.scale);
                 }
             }
         }
@@ -1249,7 +1227,8 @@ __device__ __forceinline__ void split_attention(KArgs &a, KLayer &L, int pos, in
             }
 #pragma unroll
             for (int j = 0; j < P; j++)
-                if (tb + BPJ * j < nb) sm.comb[tb + BPJ * j][tc] = __uint_as_float((uint32_t)(w[j] >> 32));
+                if (tb + BPJ * j < nb)
+                    sm.comb[tb + BPJ * j][tc] = __uint_as_float((uint32_t)(w[j] >> 32));
         }
         __syncthreads();
         if (threadIdx.x < COMB_COLS) {
