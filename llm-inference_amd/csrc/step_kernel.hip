@@ -1749,13 +1749,15 @@ struct Shape {
     // split, tokens/s): 0.6B 384 1778 / 1713, 448 1693 / 1707, 512 1480 / 1683; 1.7B 448 960 /
     // 907, 512 888 / 905; 4B 448 517 / 504, 512 488 / 511.
     static constexpr int SPLIT_BLOCKS = H <= 1024 ? 8 : 9;
-    // STEP_AUTO's switch to the hipGraph step (at most the kernel's longest history): where the
-    // split instance's per-token time crosses the graph's, measured on MI355X (64 greedy tokens
-    // after an N(0, 1) cache; split / graph tokens/s): 0.6B 4096 1374 / 1131, 8128 1154 / 1027
-    // (no crossover: the kernel runs every position it holds); 1.7B 4096 834 / 822, 6144 762 /
-    // 794; 4B 4096 479 / 466, 6144 440 / 448, 8192 428 / 432. The small test shape keeps a
-    // switch (736) so that a generate_greedy crossing it is exercised.
-    static constexpr int SWITCH_POS = H == 1024 ? 1 << 30 : H < 1024 ? 736 : 5120;
+    // STEP_AUTO's switch to the hipGraph step (at most the kernel's longest history), from the
+    // split instance's and the graph's per-token times on MI355X (64 greedy tokens after an
+    // N(0, 1) cache; split / graph tokens/s): 0.6B 4096 1450 / 1138, 8128 1213 / 1032: the
+    // kernel runs every position it holds; 1.7B 4096 850-861 / 822-826, 5120 770 / 812, 6144
+    // 780 / 794, 8128 767 / 768: the graph from 5120; 4B 4096 467-477 / 464-467, 5120 442 / 460,
+    // 6144 448 / 449, 7168 438 / 444, 8192 432-438 / 433-434: within 4% either way, so the
+    // kernel throughout (one launch per generate call). The small test shape keeps a switch
+    // (736) so that a generate_greedy crossing it is exercised.
+    static constexpr int SWITCH_POS = H == 2048 ? 5120 : H < 1024 ? 736 : 1 << 30;
     // q/k/v rows per wave (one prefetched batch; 4B: 575.4-575.9 tokens/s, 1 row 544.7) and
     // where they go. A CU's vector-memory requests complete in order, so a workgroup's poll
     // lands only after every weight request it made before the poll. At 0.6B every matrix
