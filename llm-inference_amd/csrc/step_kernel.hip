@@ -1719,7 +1719,7 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
     }
     }
     };
-    if constexpr (S::SPLIT_ROLES) {
+    if constexpr (S::SPLIT_ROLES || SPLIT) {
         if (attn_wg)
             run(std::integral_constant<int, ROLE_ATTN>{});
         else
@@ -1746,18 +1746,18 @@ struct Shape {
     // Blocks of 64 positions of history from which attention runs split over (kv head, block)
     // items (the split instance): the crossover of the two attention forms' per-token time,
     // measured on MI355X (64 greedy tokens after an N(0, 1) cache; one workgroup per head /
-    // split, tokens/s): 0.6B 384 1778 / 1713, 448 1693 / 1707, 512 1480 / 1683; 1.7B 448 960 /
-    // 907, 512 888 / 905; 4B 448 517 / 504, 512 488 / 511.
-    static constexpr int SPLIT_BLOCKS = H <= 1024 ? 8 : 9;
+    // split, tokens/s): 0.6B 384 1778 / 1713, 448 1693 / 1707, 512 1480 / 1683; 1.7B 320 1016 /
+    // 993, 384 987 / 990, 448 958 / 985; 4B 448 517 / 504, 512 488 / 511.
+    static constexpr int SPLIT_BLOCKS = H <= 1024 ? 8 : H <= 2048 ? 7 : 9;
     // STEP_AUTO's switch to the hipGraph step (at most the kernel's longest history), from the
     // split instance's and the graph's per-token times on MI355X (64 greedy tokens after an
-    // N(0, 1) cache; split / graph tokens/s): 0.6B 4096 1450 / 1138, 8128 1213 / 1032: the
-    // kernel runs every position it holds; 1.7B 4096 850-861 / 822-826, 5120 770 / 812, 6144
-    // 780 / 794, 8128 767 / 768: the graph from 5120; 4B 4096 467-477 / 464-467, 5120 442 / 460,
-    // 6144 448 / 449, 7168 438 / 444, 8192 432-438 / 433-434: within 4% either way, so the
-    // kernel throughout (one launch per generate call). The small test shape keeps a switch
-    // (736) so that a generate_greedy crossing it is exercised.
-    static constexpr int SWITCH_POS = H == 2048 ? 5120 : H < 1024 ? 736 : 1 << 30;
+    // N(0, 1) cache; split / graph tokens/s): 0.6B 4096 1450 / 1138, 8128 1213 / 1032; 1.7B
+    // 4096 865 / 826, 5120 792 / 809, 6144 791 / 792, 7168 790 / 779, 8128 802 / 766; 4B 4096
+    // 467-477 / 464-467, 5120 442 / 460, 6144 448 / 449, 7168 438 / 444, 8192 432-438 / 433-434.
+    // The graph leads by at most 4%, between ~5000 and ~7500 positions at 1.7B and 4B, so the
+    // kernel runs every position it holds (one launch per generate call). The small test shape
+    // keeps a switch (736) so that a generate_greedy crossing it is exercised.
+    static constexpr int SWITCH_POS = H < 1024 ? 736 : 1 << 30;
     // q/k/v rows per wave (one prefetched batch; 4B: 575.4-575.9 tokens/s, 1 row 544.7) and
     // where they go. A CU's vector-memory requests complete in order, so a workgroup's poll
     // lands only after every weight request it made before the poll. At 0.6B every matrix
@@ -1791,7 +1791,9 @@ struct Shape {
     static constexpr int PF_D = H <= 2048 ? PF_WITH_ATTENTION : PF_AFTER_COMPUTE;
     static constexpr int PF_QKV = H <= 1024 ? PF_WITH_ATTENTION : PF_AFTER_COMPUTE;
     // separate token loops for the two roles: 0.6B +1.7%; 1.7B -1.8% (its one shared loop
-    // spills the q/k/v prefetch to scratch memory, yet measures faster)
+    // spills the q/k/v prefetch to scratch memory, yet measures faster). The split instance
+    // always separates them (1.7B: 208 -> 52 bytes of scratch, 905 -> 979 tokens/s at 512
+    // positions, 767 -> 802 at 8128).
     static constexpr bool SPLIT_ROLES = H != 2048;
     // wave 0 of every workgroup stages the vectors and owns no matrix rows (so no weight load
     // is in flight in the polling wave); the larger shapes' vectors need every wave to poll

@@ -921,13 +921,14 @@ def test_persistent_split_attention_longest_history(gpu, oracle):
 @pytest.mark.parametrize("size", ["1.7B", "4B"])
 def test_persistent_step_wide_shapes_long_history(gpu, oracle, size):
     """The 1.7B and 4B specialisations of the persistent step (2 and 4 query heads per kv head)
-    around their switch from one workgroup per query head to the split attention (from 512
-    positions): single positions 260 and 511 (per head) and 512 (split) after a KV cache filled
+    around their switch from one workgroup per query head to the split attention (from 384 / 512
+    positions): single positions 260 and sp - 1 (per head) and sp (split) after a KV cache filled
     with N(0, 1) below them, at full widths with 2 layers; logits, argmax and the KV rows
-    written bit-identical to the oracle. Then one generate_greedy call of 16 tokens from 505,
-    which runs 505-511 in one launch of the per-head instance and 512-520 in one of the split
-    instance, continuing from the token and position the first left."""
-    ident(f"persistent step {size} widths at positions 260, 511, 512")
+    written bit-identical to the oracle. Then one generate_greedy call of 16 tokens from sp - 7,
+    which runs its first 7 tokens in one launch of the per-head instance and the rest in one of
+    the split instance, continuing from the token and position the first left."""
+    sp = {"1.7B": 384, "4B": 512}[size]
+    ident(f"persistent step {size} widths at positions 260, {sp - 1}, {sp}")
     from llm_inference_amd import model
     S = 528
     cfg = model.qwen3_config(size, n_layers=2, max_seq_len=S)
@@ -944,10 +945,10 @@ def test_persistent_step_wide_shapes_long_history(gpu, oracle, size):
         orc.bufs["key_cache"][:] = k.reshape(-1)
         orc.bufs["value_cache"][:] = v.reshape(-1)
         dec.capture_graph("auto")
-        assert dec.s.step_split_blocks == 9 and dec.s.step_switch_pos == S
+        assert dec.s.step_split_blocks == sp // 64 + 1 and dec.s.step_switch_pos == S
         dec.capture_graph("persistent")
         assert dec.persistent
-        for pos in (260, 511, 512):
+        for pos in (260, sp - 1, sp):
             tok = int(rng.integers(0, cfg.vocab_size))
             dec.forward(tok, pos)
             nxt = dec.sample_argmax()
@@ -959,10 +960,10 @@ def test_persistent_step_wide_shapes_long_history(gpu, oracle, size):
             ov = orc.bufs["value_cache"].reshape(v.shape)
             assert np.array_equal(kk[:, pos], ok[:, pos]), pos
             assert np.array_equal(vv[:, pos], ov[:, pos]), pos
-        got = dec.generate_greedy(nxt, 505, 16)
+        got = dec.generate_greedy(nxt, sp - 7, 16)
         t, want = nxt, []
         for i in range(16):
-            t = orc.forward(t, 505 + i, oracle.GPU_ORDER)
+            t = orc.forward(t, sp - 7 + i, oracle.GPU_ORDER)
             want.append(t)
         assert got == want
     finally:
