@@ -429,23 +429,30 @@ def traffic_from_profiles(tokens):
     return round(float(m.group(1)) * tokens) if m else None
 
 
-def pmc_workload(steps, size="0.6B"):
+def pmc_workload(steps, size="0.6B", prefill=0):
     """The bench's timed launch alone, for counter collection (rocprofv3 --pmc): Qwen3-`size`
     (default 0.6B, the bench step), the 5-token prompt (one launch per position), then `steps`
     greedy tokens in one launch of the persistent step kernel, then four 256 MiB device-to-device
-    copies whose FETCH_SIZE and WRITE_SIZE calibrate the counters (known bytes)."""
+    copies whose FETCH_SIZE and WRITE_SIZE calibrate the counters (known bytes). With prefill,
+    the tokens follow a KV cache whose first `prefill` positions hold N(0, 1) keys and values
+    (config_decoder's), in one launch of the kernel's split-attention instance."""
     import numpy as np
     import torch
     pkg = load_package()
     from llm_inference_amd import model
     pkg.lib()
-    cfg = model.qwen3_config(size, max_seq_len=5 + steps + 8)
-    dec = model.Decoder(cfg, ("synth", 0, 0.02, 0.1))
-    dec.capture_graph()
-    prompt = [int(t) for t in np.random.default_rng(0).integers(0, cfg.vocab_size, 5)]
-    for pos, tok in enumerate(prompt):
-        dec.forward(tok, pos)
-    dec.generate_greedy(dec.sample_argmax(), 5, steps)
+    if prefill:
+        dec, first, start, _, _, _ = config_decoder(size, prefill, steps)
+        log(f"pmc workload: {steps} tokens from position {start} ({dec.step_kind(start, steps)})")
+        dec.generate_greedy(first, start, steps)
+    else:
+        cfg = model.qwen3_config(size, max_seq_len=5 + steps + 8)
+        dec = model.Decoder(cfg, ("synth", 0, 0.02, 0.1))
+        dec.capture_graph()
+        prompt = [int(t) for t in np.random.default_rng(0).integers(0, cfg.vocab_size, 5)]
+        for pos, tok in enumerate(prompt):
+            dec.forward(tok, pos)
+        dec.generate_greedy(dec.sample_argmax(), 5, steps)
     dec.close()
     src = torch.empty(256 << 20, dtype=torch.uint8, device="cuda")
     dst = torch.empty_like(src)
@@ -464,6 +471,7 @@ def config4_workload(tokens=8):
     import torch
     load_package().lib()
     dec, first, start, _, _, _ = config_decoder("4B", 8192, tokens)
+    dec.capture_graph("graph")  # STEP_AUTO would run these positions on the step kernel
     torch.cuda.synchronize()
     log(f"config-4 workload: {tokens} tokens from position {start} "
         f"({dec.step_kind(start, tokens)})")
@@ -806,6 +814,9 @@ def main():
     ap.add_argument("--pmc-workload", nargs="?", const="0.6B", choices=["0.6B", "1.7B", "4B"],
                     help="only run the short counter-collection workload (one 256-token launch "
                          "of the step kernel; default size 0.6B)")
+    ap.add_argument("--pmc-prefill", type=int, default=0, metavar="N",
+                    help="with --pmc-workload: the tokens follow an N-position N(0, 1) KV cache "
+                         "(the step kernel's split attention)")
     ap.add_argument("--gemv-workload", action="store_true",
                     help="only launch the Qwen3-4B GEMVs at 1/8, 1/4, 1/2 and all of their rows "
                          "(for a rocprofv3 launch-cost fit and byte counters)")
@@ -828,7 +839,7 @@ def main():
         sys.exit(2)
 
     if args.pmc_workload:
-        pmc_workload(GEN_TOKENS, args.pmc_workload)
+        pmc_workload(GEN_TOKENS, args.pmc_workload, args.pmc_prefill)
     elif args.gemv_workload:
         gemv_workload()
     elif args.config4_workload:
