@@ -99,9 +99,10 @@ __device__ __forceinline__ int tid_x() {
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(tid_x() >> 6); }
 
 // The value of lane (lane ^ S), S a power of two below 64, without an LDS address: DPP
-// quad_perm for 1 and 2, ds_swizzle in bitmask mode (and 0x1f, xor S) for 4..16, and
-// v_permlane32_swap of the register with itself for 32 (afterwards the first result holds the
-// low half in both halves and the second the high half).
+// quad_perm for 1 and 2, DPP row_ror:8 for 8 (a rotation by 8 within a 16-lane row), ds_swizzle
+// in bitmask mode (and 0x1f, xor 4) for 4, and v_permlane16_swap / v_permlane32_swap of the
+// register with itself for 16 / 32 (afterwards the first result holds the even rows / the low
+// half in both rows / halves of each pair and the second the odd rows / the high half).
 template <int S>
 __device__ __forceinline__ int xor_lane(int x) {
     static_assert(S > 0 && S < 64 && (S & (S - 1)) == 0, "xor distance");
@@ -109,8 +110,13 @@ __device__ __forceinline__ int xor_lane(int x) {
         return __builtin_amdgcn_mov_dpp(x, 0xB1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
     } else if constexpr (S == 2) {
         return __builtin_amdgcn_mov_dpp(x, 0x4E, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
-    } else if constexpr (S < 32) {
+    } else if constexpr (S == 8) {
+        return __builtin_amdgcn_mov_dpp(x, 0x128, 0xf, 0xf, false);  // row_ror:8
+    } else if constexpr (S < 16) {
         return __builtin_amdgcn_ds_swizzle(x, 0x1f | (S << 10));
+    } else if constexpr (S == 16) {
+        const auto p = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+        return (tid_x() & 16) ? (int)p[0] : (int)p[1];
     } else {
         const auto p = __builtin_amdgcn_permlane32_swap(x, x, false, false);
         return (tid_x() & 32) ? (int)p[0] : (int)p[1];
@@ -121,11 +127,34 @@ __device__ __forceinline__ float xor_lane(float v) {
     return __int_as_float(xor_lane<S>(__float_as_int(v)));
 }
 
+// The two values a butterfly step at xor distance S (16 or 32) combines, own and partner in an
+// order that differs between the lanes of a pair: the swapped halves of the register with
+// itself, so no per-lane select picks the partner's value. Used with a commutative combine
+// (+, max), the result is that of own combined with partner in every lane.
+template <int S>
+__device__ __forceinline__ void swap_pair(float v, float &a, float &b) {
+    static_assert(S == 16 || S == 32, "swap distance");
+    const unsigned u = __float_as_uint(v);
+    const auto p = S == 16 ? __builtin_amdgcn_permlane16_swap(u, u, false, false)
+                           : __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    a = __uint_as_float(p[0]);
+    b = __uint_as_float(p[1]);
+}
+
 // Steps xor S, 2S, ..., N/2 of the butterfly sum.
 template <int S, int N>
 __device__ __forceinline__ float butterfly_sum(float v) {
-    if constexpr (S < N) return butterfly_sum<2 * S, N>(v + xor_lane<S>(v));
-    else return v;
+    if constexpr (S < N) {
+        if constexpr (S >= 16) {
+            float a, b;
+            swap_pair<S>(v, a, b);
+            return butterfly_sum<2 * S, N>(a + b);
+        } else {
+            return butterfly_sum<2 * S, N>(v + xor_lane<S>(v));
+        }
+    } else {
+        return v;
+    }
 }
 
 // Sum over aligned groups of N lanes by xor butterfly: lane l adds lane l^s for s = 1, 2, ...,
@@ -138,8 +167,17 @@ __device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
 
 template <int S, int N = 64>
 __device__ __forceinline__ float butterfly_max(float v) {
-    if constexpr (S < N) return butterfly_max<2 * S, N>(fmaxf(v, xor_lane<S>(v)));
-    else return v;
+    if constexpr (S < N) {
+        if constexpr (S >= 16) {
+            float a, b;
+            swap_pair<S>(v, a, b);
+            return butterfly_max<2 * S, N>(fmaxf(a, b));
+        } else {
+            return butterfly_max<2 * S, N>(fmaxf(v, xor_lane<S>(v)));
+        }
+    } else {
+        return v;
+    }
 }
 template <int N>
 __device__ __forceinline__ float group_max(float v) { return butterfly_max<1, N>(v); }
@@ -191,11 +229,24 @@ __device__ __forceinline__ float group_sum_scatter(const float (&v)[B]) {
 // at each step a lane keeps half of its values (the upper half when bit S of its lane index is
 // set) and adds its partner's copies of them, so every total has the pairing of the butterfly
 // sum; `out` receives the M * S / N values left.
+// From S = 16 on, the step swaps the rows (16) or halves (32) of values j and j + M/2 with
+// v_permlane16_swap / v_permlane32_swap: each lane receives the value it keeps and its partner's
+// copy of it, in an order that differs between the two lanes (a + b = b + a), with no select.
 template <int M, int S, int N>
 __device__ __forceinline__ void scatter_keep(const float *v, float *out) {
     if constexpr (S >= N) {
 #pragma unroll
         for (int j = 0; j < M; j++) out[j] = v[j];
+    } else if constexpr (S >= 16) {
+        float keep[M / 2];
+#pragma unroll
+        for (int j = 0; j < M / 2; j++) {
+            const unsigned a = __float_as_uint(v[j]), b = __float_as_uint(v[j + M / 2]);
+            const auto p = S == 16 ? __builtin_amdgcn_permlane16_swap(a, b, false, false)
+                                   : __builtin_amdgcn_permlane32_swap(a, b, false, false);
+            keep[j] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+        }
+        scatter_keep<M / 2, 2 * S, N>(keep, out);
     } else {
         const bool up = (tid_x() & S) != 0;
         float keep[M / 2];

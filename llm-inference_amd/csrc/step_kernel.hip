@@ -755,15 +755,9 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
             }
             // the four slot groups (lanes 16 apart) summed with the pairing of butterfly_sum<16,
             // 64> (xor 16, then xor 32), reduce-scattered: the lane ends with elements d0, d0 + 1
-            float half[4], two[2];
-            const bool up16 = (G & 1) != 0, up32 = (G & 2) != 0;
-#pragma unroll
-            for (int e = 0; e < 4; e++)
-                half[e] = (up16 ? acc[e + 4] : acc[e]) + xor_lane<16>(up16 ? acc[e] : acc[e + 4]);
-#pragma unroll
-            for (int e = 0; e < 2; e++)
-                two[e] = (up32 ? half[e + 2] : half[e]) + xor_lane<32>(up32 ? half[e] : half[e + 2]);
-            const int d0 = (up16 ? 4 : 0) + (up32 ? 2 : 0);
+            float two[2];
+            scatter_keep<8, 16, 64>(acc, two);
+            const int d0 = ((G & 1) ? 4 : 0) + ((G & 2) ? 2 : 0);
             float *qd = &sm.quarter[(w >> 2) + 2 * j][qtr][8 * Lp + d0];
             qd[0] = two[0];
             qd[1] = two[1];
@@ -866,28 +860,6 @@ __device__ __forceinline__ void split_request(KArgs &a, int pos, int pos0, int l
             kv.k[k][it] = in ? ld_kv(kc + off, t, pos0) : zero;
             kv.v[k][it] = in ? ld_kv(vc + off, t, pos0) : zero;
         }
-}
-
-// scatter_keep<M, 16, 64> (the position groups' reduce-scatter of pv_item) with
-// v_permlane16_swap and v_permlane32_swap: swapping the rows of values j and j + M/2 pairs each
-// lane with its xor-16 (then xor-32) partner as the butterfly does, and leaves in each lane the
-// half it keeps, so the sums (a + b = b + a) and the kept values are those of scatter_keep
-// without its per-lane selects.
-template <int M>
-__device__ __forceinline__ void scatter_keep_swap(const float (&v)[M], float (&out)[M / 4]) {
-    float k1[M / 2];
-#pragma unroll
-    for (int j = 0; j < M / 2; j++) {
-        const auto p = __builtin_amdgcn_permlane16_swap(
-            __float_as_uint(v[j]), __float_as_uint(v[j + M / 2]), false, false);
-        k1[j] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
-    }
-#pragma unroll
-    for (int j = 0; j < M / 4; j++) {
-        const auto p = __builtin_amdgcn_permlane32_swap(
-            __float_as_uint(k1[j]), __float_as_uint(k1[j + M / 4]), false, false);
-        out[j] = __uint_as_float(p[0]) + __uint_as_float(p[1]);
-    }
 }
 
 __device__ __forceinline__ void put_tagged64(unsigned long long *p, float v, uint32_t tag) {
@@ -1155,7 +1127,7 @@ __device__ __forceinline__ void split_attention(KArgs &a, KLayer &L, int pos, in
                 for (int r = 0; r < REP; r++)
 #pragma unroll
                     for (int e = 0; e < 8; e++) flat[r * 8 + e] = acc[r][e];
-                scatter_keep_swap<NV>(flat, kept);
+                scatter_keep<NV, 16, 64>(flat, kept);
                 int off = 0;
 #pragma unroll
                 for (int q = 0, m = NV; (16 << q) < 64; q++, m >>= 1)
