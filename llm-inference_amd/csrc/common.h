@@ -103,14 +103,17 @@ __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane
 // in bitmask mode (and 0x1f, xor 4) for 4, and v_permlane16_swap / v_permlane32_swap of the
 // register with itself for 16 / 32 (afterwards the first result holds the even rows / the low
 // half in both rows / halves of each pair and the second the odd rows / the high half).
-template <int S>
+// With LDS8 the xor-8 step is a ds_swizzle too: it then runs on the LDS unit beside the VALU,
+// which pays where many reductions run side by side (the DPP form needs two wait states and a
+// VALU move of its own), while the DPP form is shorter on a single dependent chain.
+template <int S, bool LDS8 = false>
 __device__ __forceinline__ int xor_lane(int x) {
     static_assert(S > 0 && S < 64 && (S & (S - 1)) == 0, "xor distance");
     if constexpr (S == 1) {
         return __builtin_amdgcn_mov_dpp(x, 0xB1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
     } else if constexpr (S == 2) {
         return __builtin_amdgcn_mov_dpp(x, 0x4E, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
-    } else if constexpr (S == 8) {
+    } else if constexpr (S == 8 && !LDS8) {
         return __builtin_amdgcn_mov_dpp(x, 0x128, 0xf, 0xf, false);  // row_ror:8
     } else if constexpr (S < 16) {
         return __builtin_amdgcn_ds_swizzle(x, 0x1f | (S << 10));
@@ -122,9 +125,9 @@ __device__ __forceinline__ int xor_lane(int x) {
         return (tid_x() & 32) ? (int)p[0] : (int)p[1];
     }
 }
-template <int S>
+template <int S, bool LDS8 = false>
 __device__ __forceinline__ float xor_lane(float v) {
-    return __int_as_float(xor_lane<S>(__float_as_int(v)));
+    return __int_as_float(xor_lane<S, LDS8>(__float_as_int(v)));
 }
 
 // The two values a butterfly step at xor distance S (16 or 32) combines, own and partner in an
@@ -142,15 +145,15 @@ __device__ __forceinline__ void swap_pair(float v, float &a, float &b) {
 }
 
 // Steps xor S, 2S, ..., N/2 of the butterfly sum.
-template <int S, int N>
+template <int S, int N, bool LDS8 = false>
 __device__ __forceinline__ float butterfly_sum(float v) {
     if constexpr (S < N) {
         if constexpr (S >= 16) {
             float a, b;
             swap_pair<S>(v, a, b);
-            return butterfly_sum<2 * S, N>(a + b);
+            return butterfly_sum<2 * S, N, LDS8>(a + b);
         } else {
-            return butterfly_sum<2 * S, N>(v + xor_lane<S>(v));
+            return butterfly_sum<2 * S, N, LDS8>(v + xor_lane<S, LDS8>(v));
         }
     } else {
         return v;
@@ -159,29 +162,31 @@ __device__ __forceinline__ float butterfly_sum(float v) {
 
 // Sum over aligned groups of N lanes by xor butterfly: lane l adds lane l^s for s = 1, 2, ...,
 // N/2, i.e. the balanced pairwise tree in lane order; every lane of a group ends with the sum.
-template <int N>
+template <int N, bool LDS8 = false>
 __device__ __forceinline__ float group_sum(float v) {
-    return butterfly_sum<1, N>(v);
+    return butterfly_sum<1, N, LDS8>(v);
 }
-__device__ __forceinline__ float wave_sum(float v) { return group_sum<64>(v); }
+template <bool LDS8 = false>
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<64, LDS8>(v); }
 
-template <int S, int N = 64>
+template <int S, int N = 64, bool LDS8 = false>
 __device__ __forceinline__ float butterfly_max(float v) {
     if constexpr (S < N) {
         if constexpr (S >= 16) {
             float a, b;
             swap_pair<S>(v, a, b);
-            return butterfly_max<2 * S, N>(fmaxf(a, b));
+            return butterfly_max<2 * S, N, LDS8>(fmaxf(a, b));
         } else {
-            return butterfly_max<2 * S, N>(fmaxf(v, xor_lane<S>(v)));
+            return butterfly_max<2 * S, N, LDS8>(fmaxf(v, xor_lane<S, LDS8>(v)));
         }
     } else {
         return v;
     }
 }
-template <int N>
-__device__ __forceinline__ float group_max(float v) { return butterfly_max<1, N>(v); }
-__device__ __forceinline__ float wave_max(float v) { return butterfly_max<1>(v); }
+template <int N, bool LDS8 = false>
+__device__ __forceinline__ float group_max(float v) { return butterfly_max<1, N, LDS8>(v); }
+template <bool LDS8 = false>
+__device__ __forceinline__ float wave_max(float v) { return butterfly_max<1, 64, LDS8>(v); }
 
 // Wave sums of B rows (B a power of two up to 64) with the pairing of wave_sum, so each total
 // is bit-identical to wave_sum of that row, but scattered: at step xor 2^k for k < log2(B) a
@@ -196,33 +201,33 @@ __device__ __forceinline__ int scatter_row(int lane) {
         if ((lane >> k) & 1) row += B >> (k + 1);
     return row;
 }
-template <int M, int S, int N = 64>
+template <int M, int S, int N = 64, bool LDS8 = false>
 __device__ __forceinline__ float scatter_sum_step(const float *v) {
     if constexpr (M == 1) {
-        return butterfly_sum<S, N>(v[0]);
+        return butterfly_sum<S, N, LDS8>(v[0]);
     } else {
         const bool up = (tid_x() & S) != 0;
         float keep[M / 2];
 #pragma unroll
         for (int j = 0; j < M / 2; j++) {
             const float lo = v[j], hi = v[j + M / 2];
-            const float recv = xor_lane<S>(up ? lo : hi);
+            const float recv = xor_lane<S, LDS8>(up ? lo : hi);
             keep[j] = (up ? hi : lo) + recv;
         }
-        return scatter_sum_step<M / 2, 2 * S, N>(keep);
+        return scatter_sum_step<M / 2, 2 * S, N, LDS8>(keep);
     }
 }
-template <int B>
+template <int B, bool LDS8 = false>
 __device__ __forceinline__ float wave_sum_scatter(const float (&v)[B]) {
     static_assert(B >= 1 && B <= 64 && (B & (B - 1)) == 0, "rows per batch");
-    return scatter_sum_step<B, 1>(v);
+    return scatter_sum_step<B, 1, 64, LDS8>(v);
 }
 // The same over aligned groups of N lanes: each total is bit-identical to group_sum<N> of that
 // row, and lane l ends with row scatter_row<B>(l) (B <= N).
-template <int N, int B>
+template <int N, int B, bool LDS8 = false>
 __device__ __forceinline__ float group_sum_scatter(const float (&v)[B]) {
     static_assert(B >= 1 && B <= N && N <= 64 && (B & (B - 1)) == 0, "rows per group");
-    return scatter_sum_step<B, 1, N>(v);
+    return scatter_sum_step<B, 1, N, LDS8>(v);
 }
 
 // Reduce-scatter of M values per lane over aligned lane groups of N, from xor distance S on:

@@ -1008,7 +1008,7 @@ __device__ __forceinline__ void split_attention(KArgs &a, KLayer &L, int pos, in
                     float slice[SL];
 #pragma unroll
                     for (int j = 0; j < SL; j++) slice[j] = part[s0 + j];
-                    const float d = group_sum_scatter<16, SL>(slice);
+                    const float d = group_sum_scatter<16, SL, true>(slice);
                     const int j = s0 + scatter_row<SL>(Lk), it = j / REP, r = j - it * REP;
                     if (Lk < SL)
                         sm.sc[hf][k][r][w4 * 16 + it * 4 + G] = round_bf(round_bf(d) * a.scale);
@@ -1026,9 +1026,9 @@ __device__ __forceinline__ void split_attention(KArgs &a, KLayer &L, int pos, in
                 if (b >= nb) continue;
                 const bool v = b * 64 + lane < n;
                 const float sv = v ? sm.sc[hf][k][w4][lane] : -__builtin_huge_valf();
-                const float m = wave_max(sv);
+                const float m = wave_max<true>(sv);
                 const float e = v ? exp_f32(sv - m) : 0.0f;
-                const float ssum = wave_sum(e);
+                const float ssum = wave_sum<true>(e);
                 if (lane == 0) {
                     unsigned long long *st = a.tstat + ((size_t)h * mb + b) * 2;
                     put_tagged64(st, m, tag_out);
@@ -1064,12 +1064,12 @@ __device__ __forceinline__ void split_attention(KArgs &a, KLayer &L, int pos, in
             float ml = -__builtin_huge_valf();
 #pragma unroll
             for (int c = 0; c < MAXC; c++) ml = c * 64 + lane < nb ? fmaxf(ml, mv[c]) : ml;
-            const float M = wave_max(ml);
+            const float M = wave_max<true>(ml);
             float sum = 0.0f;
 #pragma unroll
             for (int c = 0; c < MAXC; c++) {
                 if (c * 64 >= nb) break;
-                const float cs_ = wave_sum(c * 64 + lane < nb ? sv[c] * exp_f32(mv[c] - M) : 0.0f);
+                const float cs_ = wave_sum<true>(c * 64 + lane < nb ? sv[c] * exp_f32(mv[c] - M) : 0.0f);
                 sum = c == 0 ? cs_ : sum + cs_;
             }
             if (lane == 0) {
