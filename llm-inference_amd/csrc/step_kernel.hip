@@ -1332,7 +1332,8 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
     // instead of 3 on 1366: +0.8%), placed after the attention workgroups or, with
     // S::QKV_AT_END, on the last workgroups of the grid
     const int q_first = qkv_first_wg<S>((int)gridDim.x);
-    constexpr int Q_MIN = S::QKV_AT_END ? 1 : S::B_QKV;  // rows per wave at least
+    constexpr int BQ = SPLIT ? S::B_QKV_SPLIT : S::B_QKV;  // q/k/v rows per batch
+    constexpr int Q_MIN = S::QKV_AT_END ? 1 : BQ;  // rows per wave at least
     phase_rows<FW>(QD + 2 * KVD, q_first, q0, q1, Q_MIN);
     phase_rows<FW>(H, S::HQ, o0, o1);
     phase_rows<FW>(I, S::HQ, g0, g1);
@@ -1384,7 +1385,7 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
     const bool attn = ROLE == ROLE_ATTN || (ROLE == ROLE_EITHER && attn_wg);
     // The first layer's q/k/v rows of the next token, requested before the token is known
     // (by the last layer of the previous token after the first).
-    Rows<NCH, S::B_QKV> pf_qkv;
+    Rows<NCH, BQ> pf_qkv;
     NormW<H> nq;  // attn_norm weights of the coming q/k/v phase
     if (ROLE != ROLE_ATTN) {
         nq.load(klayer(kargs(), 0).attn_norm);
@@ -1466,7 +1467,7 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                 lds_chunks<NCH>(sm.vec, xb);
                 uint32_t *out = a.tqkv;
                 const uint32_t tag = tag_of(seq);
-                wave_gemv<NCH, S::B_QKV, false>(qkv_row(L), q0, q1, xb, pf_qkv,
+                wave_gemv<NCH, BQ, false>(qkv_row(L), q0, q1, xb, pf_qkv,
                                                 [=](int r, float y, uint32_t) {
                                                     const uint32_t b = f2bf(y);
                                                     put_tagged(out, r, b, tag);
@@ -1730,7 +1731,8 @@ struct Shape {
     // kernel runs every position it holds (one launch per generate call). The small test shape
     // keeps a switch (736) so that a generate_greedy crossing it is exercised.
     static constexpr int SWITCH_POS = H < 1024 ? 736 : 1 << 30;
-    // q/k/v rows per wave (one prefetched batch; 4B: 575.4-575.9 tokens/s, 1 row 544.7) and
+    // q/k/v rows per wave (a prefetched batch; 4B with batches of 2: 575.4-575.9 tokens/s, of 1
+    // row 544.7) and
     // where they go. A CU's vector-memory requests complete in order, so a workgroup's poll
     // lands only after every weight request it made before the poll. At 0.6B every matrix
     // workgroup requests its o, gate/up and down rows and the next layer's q/k/v rows while
@@ -1743,7 +1745,12 @@ struct Shape {
     // own gate/up rows request 160 KB instead of 192 KB before their gate/up poll: 2316-2333
     // against 2294-2313 (two boxes; 5 per wave +0.2%, 7 +0.5%). Spreading the o/down or gate/up
     // rows over more workgroups instead measured 1-3.5% slower (more pollers per copy).
-    static constexpr int B_QKV = H == 1024 ? 8 : H < 1024 ? 4 : 2;
+    // 4B: the wave's 4 rows in one prefetched batch, 592.0-592.3 tokens/s against 581.4-582.5
+    // with two batches of 2 (the second requested once the first is computed) and 579.6 with
+    // the second requested before it (alternating runs on one box); the split instance keeps
+    // batches of 2 (4 spill 156 bytes there)
+    static constexpr int B_QKV = H == 1024 ? 8 : H < 1024 ? 4 : H > 2048 ? 4 : 2;
+    static constexpr int B_QKV_SPLIT = H > 2048 ? 2 : B_QKV;
     static constexpr bool QKV_AT_END = H == 1024;
     static constexpr int QKV_PER_WAVE = H == 1024 ? 6 : B_QKV;
     static constexpr int B_O = H <= 1024 ? 1 : (HQ * 128 <= 2048 ? 2 : 1);
