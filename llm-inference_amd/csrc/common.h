@@ -144,16 +144,26 @@ __device__ __forceinline__ void swap_pair(float v, float &a, float &b) {
     b = __uint_as_float(p[1]);
 }
 
-// Steps xor S, 2S, ..., N/2 of the butterfly sum.
-template <int S, int N, bool LDS8 = false>
+// The partner value of the xor-4 step of a butterfly that began at xor 1: every aligned quad
+// then holds one value, so lane l ^ 7 (DPP row_half_mirror, a register move instead of an LDS
+// swizzle) holds the same value as lane l ^ 4.
+__device__ __forceinline__ float quad_partner(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xf, 0xf, false));
+}
+
+// Steps xor S, 2S, ..., N/2 of the butterfly sum. UNI: the butterfly began at xor 1 (each
+// aligned group of S lanes holds one value), which lets the xor-4 step take quad_partner.
+template <int S, int N, bool LDS8 = false, bool UNI = false>
 __device__ __forceinline__ float butterfly_sum(float v) {
     if constexpr (S < N) {
         if constexpr (S >= 16) {
             float a, b;
             swap_pair<S>(v, a, b);
-            return butterfly_sum<2 * S, N, LDS8>(a + b);
+            return butterfly_sum<2 * S, N, LDS8, UNI>(a + b);
+        } else if constexpr (S == 4 && UNI && !LDS8) {
+            return butterfly_sum<2 * S, N, LDS8, UNI>(v + quad_partner(v));
         } else {
-            return butterfly_sum<2 * S, N, LDS8>(v + xor_lane<S, LDS8>(v));
+            return butterfly_sum<2 * S, N, LDS8, UNI>(v + xor_lane<S, LDS8>(v));
         }
     } else {
         return v;
@@ -164,29 +174,31 @@ __device__ __forceinline__ float butterfly_sum(float v) {
 // N/2, i.e. the balanced pairwise tree in lane order; every lane of a group ends with the sum.
 template <int N, bool LDS8 = false>
 __device__ __forceinline__ float group_sum(float v) {
-    return butterfly_sum<1, N, LDS8>(v);
+    return butterfly_sum<1, N, LDS8, true>(v);
 }
 template <bool LDS8 = false>
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<64, LDS8>(v); }
 
-template <int S, int N = 64, bool LDS8 = false>
+template <int S, int N = 64, bool LDS8 = false, bool UNI = false>
 __device__ __forceinline__ float butterfly_max(float v) {
     if constexpr (S < N) {
         if constexpr (S >= 16) {
             float a, b;
             swap_pair<S>(v, a, b);
-            return butterfly_max<2 * S, N, LDS8>(fmaxf(a, b));
+            return butterfly_max<2 * S, N, LDS8, UNI>(fmaxf(a, b));
+        } else if constexpr (S == 4 && UNI && !LDS8) {
+            return butterfly_max<2 * S, N, LDS8, UNI>(fmaxf(v, quad_partner(v)));
         } else {
-            return butterfly_max<2 * S, N, LDS8>(fmaxf(v, xor_lane<S, LDS8>(v)));
+            return butterfly_max<2 * S, N, LDS8, UNI>(fmaxf(v, xor_lane<S, LDS8>(v)));
         }
     } else {
         return v;
     }
 }
 template <int N, bool LDS8 = false>
-__device__ __forceinline__ float group_max(float v) { return butterfly_max<1, N, LDS8>(v); }
+__device__ __forceinline__ float group_max(float v) { return butterfly_max<1, N, LDS8, true>(v); }
 template <bool LDS8 = false>
-__device__ __forceinline__ float wave_max(float v) { return butterfly_max<1, 64, LDS8>(v); }
+__device__ __forceinline__ float wave_max(float v) { return butterfly_max<1, 64, LDS8, true>(v); }
 
 // Wave sums of B rows (B a power of two up to 64) with the pairing of wave_sum, so each total
 // is bit-identical to wave_sum of that row, but scattered: at step xor 2^k for k < log2(B) a
@@ -204,7 +216,7 @@ __device__ __forceinline__ int scatter_row(int lane) {
 template <int M, int S, int N = 64, bool LDS8 = false>
 __device__ __forceinline__ float scatter_sum_step(const float *v) {
     if constexpr (M == 1) {
-        return butterfly_sum<S, N, LDS8>(v[0]);
+        return butterfly_sum<S, N, LDS8, S == 1>(v[0]);
     } else {
         const bool up = (tid_x() & S) != 0;
         float keep[M / 2];
