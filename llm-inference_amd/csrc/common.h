@@ -99,13 +99,15 @@ __device__ __forceinline__ int tid_x() {
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(tid_x() >> 6); }
 
 // The value of lane (lane ^ S), S a power of two below 64, without an LDS address: DPP
-// quad_perm for 1 and 2, DPP row_ror:8 for 8 (a rotation by 8 within a 16-lane row), ds_swizzle
-// in bitmask mode (and 0x1f, xor 4) for 4, and v_permlane16_swap / v_permlane32_swap of the
-// register with itself for 16 / 32 (afterwards the first result holds the even rows / the low
-// half in both rows / halves of each pair and the second the odd rows / the high half).
-// With LDS8 the xor-8 step is a ds_swizzle too: it then runs on the LDS unit beside the VALU,
-// which pays where many reductions run side by side (the DPP form needs two wait states and a
-// VALU move of its own), while the DPP form is shorter on a single dependent chain.
+// quad_perm for 1 and 2; for 4 two DPP moves into one register, row_shl:4 (lane l reads
+// l + 4) into banks 0 and 2 (lanes 0-3 and 8-11 of each 16-lane row) and row_shr:4 (l - 4)
+// into banks 1 and 3; DPP row_ror:8 for 8 (a rotation by 8 within a row); v_permlane16_swap /
+// v_permlane32_swap of the register with itself for 16 / 32 (afterwards the first result holds
+// the even rows / the low half in both rows / halves of each pair and the second the odd rows /
+// the high half). With LDS8 the xor-4 and xor-8 steps are ds_swizzles (bitmask mode: and 0x1f,
+// xor S): they then run on the LDS unit beside the VALU, which pays where many reductions run
+// side by side (the DPP forms need wait states and VALU moves of their own), while the DPP forms
+// are shorter on a single dependent chain.
 template <int S, bool LDS8 = false>
 __device__ __forceinline__ int xor_lane(int x) {
     static_assert(S > 0 && S < 64 && (S & (S - 1)) == 0, "xor distance");
@@ -113,6 +115,9 @@ __device__ __forceinline__ int xor_lane(int x) {
         return __builtin_amdgcn_mov_dpp(x, 0xB1, 0xf, 0xf, false);  // quad_perm [1,0,3,2]
     } else if constexpr (S == 2) {
         return __builtin_amdgcn_mov_dpp(x, 0x4E, 0xf, 0xf, false);  // quad_perm [2,3,0,1]
+    } else if constexpr (S == 4 && !LDS8) {
+        const int t = __builtin_amdgcn_update_dpp(x, x, 0x104, 0xf, 0x5, false);  // row_shl:4
+        return __builtin_amdgcn_update_dpp(t, x, 0x114, 0xf, 0xA, false);         // row_shr:4
     } else if constexpr (S == 8 && !LDS8) {
         return __builtin_amdgcn_mov_dpp(x, 0x128, 0xf, 0xf, false);  // row_ror:8
     } else if constexpr (S < 16) {
@@ -200,6 +205,25 @@ __device__ __forceinline__ float group_max(float v) { return butterfly_max<1, N,
 template <bool LDS8 = false>
 __device__ __forceinline__ float wave_max(float v) { return butterfly_max<1, 64, LDS8, true>(v); }
 
+// One reduce-scatter step at xor S = 4 or 8 (lanes whose bit S is clear keep lo, the others
+// hi), with no per-lane select: two DPP moves fill one register with the partner's copy of the
+// value each lane keeps, selecting by bank (4 lanes) which lanes each move writes: at S = 4
+// row_shl:4 (lane l reads l + 4) into banks 0 and 2 over the lane's own hi, and row_shr:4 (l - 4)
+// into banks 1 and 3 over its own lo; at S = 8 row_ror:8 into banks 0-1, then into banks 2-3.
+// The sum is own + partner (in an order that differs between the two lanes of a pair).
+template <int S>
+__device__ __forceinline__ float bank_pair_sum(float lo, float hi) {
+    static_assert(S == 4 || S == 8, "bank-selected exchange");
+    constexpr int LOW = S == 4 ? 0x5 : 0x3, HIGH = S == 4 ? 0xA : 0xC;
+    constexpr int FROM_UP = S == 4 ? 0x104 : 0x128, FROM_DOWN = S == 4 ? 0x114 : 0x128;
+    const int l = __float_as_int(lo), h = __float_as_int(hi);
+    // banks of the lower lanes: the partner's lo; the upper lanes: their own hi
+    const int a = __builtin_amdgcn_update_dpp(h, l, FROM_UP, 0xf, LOW, false);
+    // banks of the upper lanes: the partner's hi; the lower lanes: their own lo
+    const int b = __builtin_amdgcn_update_dpp(l, h, FROM_DOWN, 0xf, HIGH, false);
+    return __int_as_float(a) + __int_as_float(b);
+}
+
 // Wave sums of B rows (B a power of two up to 64) with the pairing of wave_sum, so each total
 // is bit-identical to wave_sum of that row, but scattered: at step xor 2^k for k < log2(B) a
 // lane keeps half of its rows (the upper half when bit k of its lane index is set) and adds
@@ -213,7 +237,7 @@ __device__ __forceinline__ int scatter_row(int lane) {
         if ((lane >> k) & 1) row += B >> (k + 1);
     return row;
 }
-template <int M, int S, int N = 64, bool LDS8 = false>
+template <int M, int S, int N = 64, bool LDS8 = false, bool BANK = false>
 __device__ __forceinline__ float scatter_sum_step(const float *v) {
     if constexpr (M == 1) {
         return butterfly_sum<S, N, LDS8, S == 1>(v[0]);
@@ -223,16 +247,21 @@ __device__ __forceinline__ float scatter_sum_step(const float *v) {
 #pragma unroll
         for (int j = 0; j < M / 2; j++) {
             const float lo = v[j], hi = v[j + M / 2];
-            const float recv = xor_lane<S, LDS8>(up ? lo : hi);
-            keep[j] = (up ? hi : lo) + recv;
+            if constexpr ((S == 4 || S == 8) && BANK && !LDS8) {
+                keep[j] = bank_pair_sum<S>(lo, hi);
+            } else {
+                const float recv = xor_lane<S, LDS8>(up ? lo : hi);
+                keep[j] = (up ? hi : lo) + recv;
+            }
         }
-        return scatter_sum_step<M / 2, 2 * S, N, LDS8>(keep);
+        return scatter_sum_step<M / 2, 2 * S, N, LDS8, BANK>(keep);
     }
 }
-template <int B, bool LDS8 = false>
+// BANK: the xor-4 and xor-8 steps through bank_pair_sum (no per-lane select).
+template <int B, bool LDS8 = false, bool BANK = false>
 __device__ __forceinline__ float wave_sum_scatter(const float (&v)[B]) {
     static_assert(B >= 1 && B <= 64 && (B & (B - 1)) == 0, "rows per batch");
-    return scatter_sum_step<B, 1, 64, LDS8>(v);
+    return scatter_sum_step<B, 1, 64, LDS8, BANK>(v);
 }
 // The same over aligned groups of N lanes: each total is bit-identical to group_sum<N> of that
 // row, and lane l ends with row scatter_row<B>(l) (B <= N).

@@ -280,8 +280,11 @@ struct LdsX {
 };
 
 // The B row sums of a batch against xin (gemv_kernel arithmetic: per-lane fma over the chunks
-// in order, then the wave tree); lane l gets row scatter_row<B>(l) of the batch.
-template <int NC, int B, class X>
+// in order, then the wave tree); lane l gets row scatter_row<B>(l) of the batch. BANK: the
+// reduce-scatter's xor-4 and xor-8 steps without per-lane selects (the split instance: 0.6B
+// after 8192 positions 1215 -> 1227 tokens/s; the one-head-per-workgroup instance at 0.6B
+// measured 0.3% slower with it, at 1.7B and 4B the same).
+template <bool BANK = false, int NC, int B, class X>
 __device__ __forceinline__ float batch_sums(const Rows<NC, B> &b, const X &xin) {
     float part[B];
 #pragma unroll
@@ -300,7 +303,7 @@ __device__ __forceinline__ float batch_sums(const Rows<NC, B> &b, const X &xin) 
 #pragma unroll
             for (int k = 0; k < NC; k++) part[i] = dot8(b.w[i][k], xin[k], part[i]);
     }
-    return wave_sum_scatter<B>(part);
+    return wave_sum_scatter<B, false, BANK>(part);
 }
 
 
@@ -311,7 +314,8 @@ __device__ __forceinline__ float batch_sums(const Rows<NC, B> &b, const X &xin) 
 // (lane j: row r0 + j, at most 64 rows): with KEEP it is replaced by epi's result for the row,
 // so a wave carries the residual rows it updates from one phase to the next. Lane
 // scatter_row<B>(k) computes batch row k, and scatter_row<B> is its own inverse.
-template <int NC, int B, bool STREAM, bool KEEP = false, class RowP, class X, class Epi>
+template <int NC, int B, bool STREAM, bool KEEP = false, bool BANK = false, class RowP, class X,
+          class Epi>
 __device__ __forceinline__ void wave_gemv(RowP rowp, int r0, int r1, const X &xin,
                                           Rows<NC, B> &cur, Epi epi, uint32_t *own = nullptr) {
     const int lane = tid_x() & 63;
@@ -331,19 +335,19 @@ __device__ __forceinline__ void wave_gemv(RowP rowp, int r0, int r1, const X &xi
         Rows<NC, B> nxt;
         for (int r = r0; r < r1; r += 2 * B) {
             if (r + B < r1) nxt.load(rowp, r + B, r1);
-            finish(batch_sums(cur, xin), r);
+            finish(batch_sums<BANK>(cur, xin), r);
             if (r + B >= r1) break;
             if (r + 2 * B < r1) cur.load(rowp, r + 2 * B, r1);
-            finish(batch_sums(nxt, xin), r + B);
+            finish(batch_sums<BANK>(nxt, xin), r + B);
         }
     } else {
         // the first batch outside the loop: a loop head would merge this batch's (long
         // complete) registers with the loads of the loop's back edge, and the wait placed there
         // would then also wait for every request issued since the prefetch
-        if (r0 < r1) finish(batch_sums(cur, xin), r0);
+        if (r0 < r1) finish(batch_sums<BANK>(cur, xin), r0);
         for (int r = r0 + B; r < r1; r += B) {
             cur.load(rowp, r, r1);
-            finish(batch_sums(cur, xin), r);
+            finish(batch_sums<BANK>(cur, xin), r);
         }
     }
 }
@@ -351,7 +355,7 @@ __device__ __forceinline__ void wave_gemv(RowP rowp, int r0, int r1, const X &xi
 // gate and up rows together (gate_up_kernel arithmetic); first batch preloaded. With STREAM the
 // next batch is requested before the current one is computed (two batches in flight), else
 // after.
-template <int NC, int B, bool STREAM, class Epi>
+template <int NC, int B, bool STREAM, bool BANK = false, class Epi>
 __device__ __forceinline__ void wave_gemv2(const bf16 *Wg, const bf16 *Wu, int r0, int r1,
                                            const u32x4 (&xin)[NC], Rows<NC, B> &gb,
                                            Rows<NC, B> &ub, Epi epi) {
@@ -360,7 +364,7 @@ __device__ __forceinline__ void wave_gemv2(const bf16 *Wg, const bf16 *Wu, int r
     auto g_row = [&](int rr) { return Wg + (size_t)rr * COLS; };
     auto u_row = [&](int rr) { return Wu + (size_t)rr * COLS; };
     auto finish = [&](const Rows<NC, B> &g, const Rows<NC, B> &u, int r) {
-        const float tg = batch_sums(g, xin), tu = batch_sums(u, xin);
+        const float tg = batch_sums<BANK>(g, xin), tu = batch_sums<BANK>(u, xin);
         const int row = r + scatter_row<B>(lane);
         if (lane < B && row < r1) epi(row, tg, tu);
     };
@@ -1467,7 +1471,7 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                 lds_chunks<NCH>(sm.vec, xb);
                 uint32_t *out = a.tqkv;
                 const uint32_t tag = tag_of(seq);
-                wave_gemv<NCH, BQ, false>(qkv_row(L), q0, q1, xb, pf_qkv,
+                wave_gemv<NCH, BQ, false, false, SPLIT>(qkv_row(L), q0, q1, xb, pf_qkv,
                                                 [=](int r, float y, uint32_t) {
                                                     const uint32_t b = f2bf(y);
                                                     put_tagged(out, r, b, tag);
@@ -1517,7 +1521,7 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                 if (o0 < o1) {
                     u32x4 in[NCO];
                     lds_chunks<NCO>(sm.vec, in);
-                    wave_gemv<NCO, S::B_O, S::O_STREAM, true>(
+                    wave_gemv<NCO, S::B_O, S::O_STREAM, true, SPLIT>(
                         o_row(klayer(kargs(), l)), o0, o1, in, pf_o,
                         residual(out_stage, wr0, tag_of(seq + 2)), &xown);
                 }
@@ -1544,7 +1548,7 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                 lds_chunks<NCH>(sm.vec, xb);
                 uint32_t *hb = a.thb;
                 const uint32_t tag = tag_of(seq + 3);
-                wave_gemv2<NCH, S::B_GU, S::GU_STREAM>(L.w_gate, L.w_up, g0, g1, xb, pf_g, pf_u,
+                wave_gemv2<NCH, S::B_GU, S::GU_STREAM, SPLIT>(L.w_gate, L.w_up, g0, g1, xb, pf_g, pf_u,
                                          [=](int r, float g, float u) {
                     const bf16 gb = (bf16)f2bf(g), ub = (bf16)f2bf(u);
                     const float s = round_bf(silu_f32(bf2f(gb)));
@@ -1562,13 +1566,13 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
             if (wg_o) {
                 if (o0 < o1) {
                     if constexpr (S::X_LDS_DOWN) {
-                        wave_gemv<NCI, S::B_DOWN, S::D_STREAM, true>(
+                        wave_gemv<NCI, S::B_DOWN, S::D_STREAM, true, SPLIT>(
                             d_row(klayer(kargs(), l)), o0, o1, LdsX{(const u32x4 *)sm.vec}, pf_d,
                             residual(out_stage, wr0, tag_of(seq + 4)), &xown);
                     } else {
                         u32x4 in[NCI];
                         lds_chunks<NCI>(sm.vec, in);
-                        wave_gemv<NCI, S::B_DOWN, S::D_STREAM, true>(
+                        wave_gemv<NCI, S::B_DOWN, S::D_STREAM, true, SPLIT>(
                             d_row(klayer(kargs(), l)), o0, o1, in, pf_d,
                             residual(out_stage, wr0, tag_of(seq + 4)), &xown);
                     }
@@ -1607,7 +1611,7 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
             u32x4 xb[NCH];
             lds_chunks<NCH>(sm.vec, xb);
             bf16 *logits = a.logits;
-            wave_gemv<NCH, S::B_LM, true>(lm_row, r0, r1, xb, batch,
+            wave_gemv<NCH, S::B_LM, true, false, SPLIT>(lm_row, r0, r1, xb, batch,
                                           [&](int r, float y, uint32_t) {
                 const uint32_t yb = f2bf(y);
                 gptr(logits)[r] = (bf16)yb;
