@@ -265,10 +265,10 @@ __device__ __forceinline__ float wave_sum_scatter(const float (&v)[B]) {
 }
 // The same over aligned groups of N lanes: each total is bit-identical to group_sum<N> of that
 // row, and lane l ends with row scatter_row<B>(l) (B <= N).
-template <int N, int B, bool LDS8 = false>
+template <int N, int B, bool LDS8 = false, bool BANK = false>
 __device__ __forceinline__ float group_sum_scatter(const float (&v)[B]) {
     static_assert(B >= 1 && B <= N && N <= 64 && (B & (B - 1)) == 0, "rows per group");
-    return scatter_sum_step<B, 1, N, LDS8>(v);
+    return scatter_sum_step<B, 1, N, LDS8, BANK>(v);
 }
 
 // Reduce-scatter of M values per lane over aligned lane groups of N, from xor distance S on:

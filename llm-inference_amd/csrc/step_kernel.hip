@@ -645,7 +645,7 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
                 const int t = key_slot(base, u);
                 part[u] = dot8(qv, base == 0 ? (t == pos ? kcur : pre.k[u]) : kv[u], 0.0f);
             }
-            const float d = group_sum_scatter<16>(part);
+            const float d = group_sum_scatter<16, SCORE_LOADS, false, true>(part);
             const int t = key_slot(base, us);
             if (Lp < SCORE_LOADS && t < n) sm.sc[t] = round_bf(round_bf(d) * a.scale);
         }
@@ -1012,7 +1012,7 @@ __device__ __forceinline__ void split_attention(KArgs &a, KLayer &L, int pos, in
                     float slice[SL];
 #pragma unroll
                     for (int j = 0; j < SL; j++) slice[j] = part[s0 + j];
-                    const float d = group_sum_scatter<16, SL, true>(slice);
+                    const float d = group_sum_scatter<16, SL, false, true>(slice);
                     const int j = s0 + scatter_row<SL>(Lk), it = j / REP, r = j - it * REP;
                     if (Lk < SL)
                         sm.sc[hf][k][r][w4 * 16 + it * 4 + G] = round_bf(round_bf(d) * a.scale);
@@ -1030,9 +1030,9 @@ __device__ __forceinline__ void split_attention(KArgs &a, KLayer &L, int pos, in
                 if (b >= nb) continue;
                 const bool v = b * 64 + lane < n;
                 const float sv = v ? sm.sc[hf][k][w4][lane] : -__builtin_huge_valf();
-                const float m = wave_max<true>(sv);
+                const float m = wave_max<S::SPLIT_STATS_LDS>(sv);
                 const float e = v ? exp_f32(sv - m) : 0.0f;
-                const float ssum = wave_sum<true>(e);
+                const float ssum = wave_sum<S::SPLIT_STATS_LDS>(e);
                 if (lane == 0) {
                     unsigned long long *st = a.tstat + ((size_t)h * mb + b) * 2;
                     put_tagged64(st, m, tag_out);
@@ -1068,12 +1068,12 @@ __device__ __forceinline__ void split_attention(KArgs &a, KLayer &L, int pos, in
             float ml = -__builtin_huge_valf();
 #pragma unroll
             for (int c = 0; c < MAXC; c++) ml = c * 64 + lane < nb ? fmaxf(ml, mv[c]) : ml;
-            const float M = wave_max<true>(ml);
+            const float M = wave_max<S::SPLIT_STATS_LDS>(ml);
             float sum = 0.0f;
 #pragma unroll
             for (int c = 0; c < MAXC; c++) {
                 if (c * 64 >= nb) break;
-                const float cs_ = wave_sum<true>(c * 64 + lane < nb ? sv[c] * exp_f32(mv[c] - M) : 0.0f);
+                const float cs_ = wave_sum<S::SPLIT_STATS_LDS>(c * 64 + lane < nb ? sv[c] * exp_f32(mv[c] - M) : 0.0f);
                 sum = c == 0 ? cs_ : sum + cs_;
             }
             if (lane == 0) {
@@ -1735,6 +1735,12 @@ struct Shape {
     // kernel runs every position it holds (one launch per generate call). The small test shape
     // keeps a switch (736) so that a generate_greedy crossing it is exercised.
     static constexpr int SWITCH_POS = H < 1024 ? 736 : 1 << 30;
+    // The split attention's statistics (block and global max and sum) reduce with their xor-4
+    // and xor-8 steps through ds_swizzle (LDS8) where two query heads share a kv head, through
+    // DPP at 4B (four): 0.6B after 8192 positions 1235-1237 tokens/s against 1185-1194 with DPP;
+    // 4B 441.8-441.9 against 439.0-439.1 with the swizzle (the scores' reduce-scatter through
+    // bank_pair_sum in both; alternating runs on one box).
+    static constexpr bool SPLIT_STATS_LDS = H <= 2048;
     // q/k/v rows per wave (a prefetched batch; 4B with batches of 2: 575.4-575.9 tokens/s, of 1
     // row 544.7) and
     // where they go. A CU's vector-memory requests complete in order, so a workgroup's poll
