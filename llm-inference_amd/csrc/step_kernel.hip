@@ -1764,8 +1764,11 @@ struct Shape {
     // last 64: 2300-2323 against 2282-2292 tokens/s (alternating runs on four boxes); 6 per
     // wave (one batch of 8 with two empty rows) on the last 86, so that the 38 of them that also
     // own gate/up rows request 160 KB instead of 192 KB before their gate/up poll: 2316-2333
-    // against 2294-2313 (two boxes; 5 per wave +0.2%, 7 +0.5%). Spreading the o/down or gate/up
-    // rows over more workgroups instead measured 1-3.5% slower (more pollers per copy).
+    // against 2294-2313 (two boxes; 5 per wave +0.2%, 7 +0.5%). After the reductions' lane
+    // exchanges were shortened, 7 per wave on the last 74 measured 2428.4-2428.9 against
+    // 2425.0-2425.9 for 6 and 2421.5-2423.9 for 5 (alternating runs on one box), so 7 is kept.
+    // Spreading the o/down or gate/up rows over more workgroups instead measured 1-3.5% slower
+    // (more pollers per copy).
     // 4B: the wave's 4 rows in one prefetched batch, 592.0-592.3 tokens/s against 581.4-582.5
     // with two batches of 2 (the second requested once the first is computed) and 579.6 with
     // the second requested before it (alternating runs on one box); the split instance keeps
@@ -1773,7 +1776,7 @@ struct Shape {
     static constexpr int B_QKV = H == 1024 ? 8 : H < 1024 ? 4 : H > 2048 ? 4 : 2;
     static constexpr int B_QKV_SPLIT = H > 2048 ? 2 : B_QKV;
     static constexpr bool QKV_AT_END = H == 1024;
-    static constexpr int QKV_PER_WAVE = H == 1024 ? 6 : B_QKV;
+    static constexpr int QKV_PER_WAVE = H == 1024 ? 7 : B_QKV;
     static constexpr int B_O = H <= 1024 ? 1 : (HQ * 128 <= 2048 ? 2 : 1);
     static constexpr int B_GU = H <= 1024 ? 2 : 1;
     static constexpr int B_DOWN = 1;
