@@ -565,17 +565,18 @@ def phase_trace(positions=range(8, 40), size="0.6B"):
                                    ctypes.POINTER(ctypes.c_longlong))
     # rows per matrix workgroup (8 waves each, HQ attention workgroups own none): the rows of
     # the kernel's phase_rows, to know which workgroups take part in a phase. The q/k/v rows
-    # come in batches of B_QKV per wave (4 below hidden 1024, 2 above) or, at hidden 1024, 6 per
-    # wave on the last workgroups of the grid (qkv_first_wg).
+    # come in batches of B_QKV per wave (4 below hidden 1024 and above 2048, 2 at 2048) or, at
+    # hidden 1024, 7 per wave on the last workgroups of the grid (Shape::QKV_PER_WAVE,
+    # qkv_first_wg).
     def owners(R, min_per=1, first=hq):
         per = max(-(-R // ((grid - first) * 8)), min_per)
         return [b for b in range(first, grid) if (b - first) * 8 * per < R]
 
     qd, kvd = hq * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
     if cfg.hidden_size == 1024:
-        q_min, q_first = 1, grid - -(-(qd + 2 * kvd) // (8 * 6))
+        q_min, q_first = 1, grid - -(-(qd + 2 * kvd) // (8 * 7))
     else:
-        q_min, q_first = (4 if cfg.hidden_size < 1024 else 2), hq
+        q_min, q_first = (2 if cfg.hidden_size == 2048 else 4), hq
     part = {"q/k/v rows (RMSNorm + GEMV)": (0, owners(qd + 2 * kvd, q_min, q_first)),
             "attention (one head per workgroup)": (0, list(range(hq))),
             "o rows + residual": (1, owners(cfg.hidden_size)),
