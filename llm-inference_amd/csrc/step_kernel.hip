@@ -1656,13 +1656,25 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
             KArgs &a = kargs();
             float v = -__builtin_huge_valf();
             int idx = INT_MAX;
-            for (int k = lane; k < (int)gridDim.x; k += 64)
-                amax_pair(v, idx,
-                          __uint_as_float(__hip_atomic_load(gptr((unsigned *)&a.amax_val[k]),
-                                                            __ATOMIC_RELAXED,
-                                                            __HIP_MEMORY_SCOPE_AGENT)),
-                          __hip_atomic_load(gptr(&a.amax_idx[k]), __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT));
+            // every partial of a round of 256 requested before any is compared (one loop step per
+            // 64 partials would wait for each step's loads in turn), then compared in the order
+            // k = lane, lane + 64, ...; a lane past the grid reads partial 0 and ignores it
+            for (int k0 = 0; k0 < (int)gridDim.x; k0 += 4 * 64) {
+                float pv[4];
+                int pi[4];
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int k = k0 + lane + 64 * j, kk = k < (int)gridDim.x ? k : 0;
+                    pv[j] = __uint_as_float(__hip_atomic_load(gptr((unsigned *)&a.amax_val[kk]),
+                                                              __ATOMIC_RELAXED,
+                                                              __HIP_MEMORY_SCOPE_AGENT));
+                    pi[j] = __hip_atomic_load(gptr(&a.amax_idx[kk]), __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+                }
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    if (k0 + lane + 64 * j < (int)gridDim.x) amax_pair(v, idx, pv[j], pi[j]);
+            }
             wave_amax(v, idx);
             if (lane == 0) {
                 *gptr(a.next_token) = idx;
