@@ -31,7 +31,8 @@ struct StepArgs {
     int *next_token, *pos, *token_out, *pos_base, *error_flag;
     unsigned *epoch;      // tagged phases written over all launches (the tag base)
     unsigned *final_ctr;  // workgroups done with the LM head (counts over a launch's tokens)
-    unsigned long long *token_word;  // the next token, tagged: (token << 32) | tag
+    // the next token, tagged ((token << 32) | tag), in TOKEN_COPIES copies 64 words apart
+    unsigned long long *token_word;
     float *amax_val;      // per-workgroup argmax partials
     int *amax_idx;
     long long *trace;     // optional wall-clock stamps of one workgroup's phases
@@ -45,16 +46,23 @@ struct StepArgs {
     float inv_freq[64];
 };
 
+// The next token reaches every workgroup as a tagged word in up to TOKEN_COPIES copies 512 bytes
+// apart, away from the cache line of final_ctr, which every workgroup adds to once per token (a
+// shape that uses R copies has workgroup b poll copy b % R).
+constexpr int TOKEN_COPIES = 8;
+
 // Workspace the step kernel keeps in RunState::step_ws (zeroed at allocation and after an
-// error; a zero tag never matches), followed by the tagged vectors.
+// error; a zero tag never matches), followed by the tagged vectors. Its size is 256 bytes past a
+// multiple of 4 KB, which places the tagged vectors' copies 1 KB off the 4 KB grid.
 struct StepWorkspace {
     unsigned epoch;
     unsigned final_ctr;
-    unsigned long long token_word;
-    unsigned pad[60];
+    unsigned pad[62];
+    unsigned long long token_word[TOKEN_COPIES][64];  // copy c at token_word[c][0]
     float amax_val[1024];
     int amax_idx[1024];
 };
+static_assert(sizeof(StepWorkspace) % 4096 == 256, "tagged vectors 256 bytes past the 4 KB grid");
 
 // The workspace for a run state of max_seq positions: the words above, the tagged vectors, then
 // the split attention's statistics and partials.

@@ -1676,6 +1676,12 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                     if (k0 + lane + 64 * j < (int)gridDim.x) amax_pair(v, idx, pv[j], pi[j]);
             }
             wave_amax(v, idx);
+            if (step + 1 < n_tokens && lane < S::TOKEN_COPIES) {
+                // the next token for every workgroup, one copy per lane
+                __hip_atomic_store(gptr(a.token_word + 64 * lane),
+                                   ((unsigned long long)(unsigned)idx << 32) | tag_of(seq_end),
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
             if (lane == 0) {
                 *gptr(a.next_token) = idx;
                 if (a.advance) {
@@ -1683,12 +1689,7 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                     if (i >= 0 && i < a.token_capacity) gptr(a.token_out)[i] = idx;
                     *gptr(a.pos) = pos + 1;
                 }
-                if (step + 1 < n_tokens) {
-                    // the next token for every workgroup
-                    __hip_atomic_store(gptr(a.token_word),
-                                       ((unsigned long long)(unsigned)idx << 32) | tag_of(seq_end),
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                } else {
+                if (step + 1 >= n_tokens) {
                     *gptr(a.final_ctr) = 0;
                     *gptr(a.epoch) = seq0 + n_tokens * seq_step;
                     if (a.trace) gptr(a.trace)[2 + 4 * n_layers] = wall_clock64();
@@ -1703,8 +1704,9 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                 unsigned long long tw = 0;
                 long long spins = 0;
                 for (;;) {
-                    tw = __hip_atomic_load(gptr(a.token_word), __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
+                    tw = __hip_atomic_load(
+                        gptr(a.token_word + 64 * ((int)blockIdx.x % S::TOKEN_COPIES)),
+                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     if ((uint32_t)tw == tag_of(seq_end)) break;
                     if ((++spins & 63) == 0 && wait_gives_up(spins, SPIN_LIMIT, a.error_flag))
                         break;
@@ -1800,6 +1802,11 @@ struct Shape {
     // 2 copies 2258); before that layout 4 measured faster (2291-2294 against 2280-2282 with 8,
     // 2301 against 2221 with 2 and 2067 with 3). 1.7B and 4B: 4 (1.7B 1115 against 1074 with 8).
     static constexpr int REPLICAS = H == 1024 ? 8 : 4;
+    // copies of the next token's word the workgroups poll (at most TOKEN_COPIES), each on a
+    // cache line of its own: 0.6B 2486.4 tokens/s with one, 2478.3 with 8, 2417.6 when the one
+    // word shared the cache line of the counter every workgroup adds to once per token
+    // (alternating runs on one box); 4B 596.8 with 8 against 594.7 with one
+    static constexpr int TOKEN_COPIES = H <= 1024 ? 1 : 8;
     // 1.7B: the down rows with attention 1050 -> 1075 tokens/s, the q/k/v rows too 1005; 4B
     // (5-token prompt): 575.8-576.4 as below, the q/k/v rows after the gate/up poll 572.6-572.8,
     // the down rows after the o poll 466.2-466.3
