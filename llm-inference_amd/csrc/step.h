@@ -33,8 +33,8 @@ struct StepArgs {
     unsigned *final_ctr;  // workgroups done with the LM head (counts over a launch's tokens)
     // the next token, tagged ((token << 32) | tag), in TOKEN_COPIES copies 64 words apart
     unsigned long long *token_word;
-    float *amax_val;      // per-workgroup argmax partials
-    int *amax_idx;
+    // per-workgroup argmax partials, (float bits << 32) | index, AMAX_STRIDE words apart
+    unsigned long long *amax;
     long long *trace;     // optional wall-clock stamps of one workgroup's phases
     float eps, scale;
     int n_layers, vocab, max_seq, token_capacity, advance;
@@ -50,6 +50,9 @@ struct StepArgs {
 // apart, away from the cache line of final_ctr, which every workgroup adds to once per token (a
 // shape that uses R copies has workgroup b poll copy b % R).
 constexpr int TOKEN_COPIES = 8;
+// Each workgroup's argmax partial (one 64-bit word) sits on a 128-byte line of its own, so the
+// workgroups' stores at the end of a token do not meet on shared lines.
+constexpr int AMAX_STRIDE = 16;
 
 // Workspace the step kernel keeps in RunState::step_ws (zeroed at allocation and after an
 // error; a zero tag never matches), followed by the tagged vectors. Its size is 256 bytes past a
@@ -59,8 +62,7 @@ struct StepWorkspace {
     unsigned final_ctr;
     unsigned pad[62];
     unsigned long long token_word[TOKEN_COPIES][64];  // copy c at token_word[c][0]
-    float amax_val[1024];
-    int amax_idx[1024];
+    unsigned long long amax[1024 * AMAX_STRIDE];      // workgroup b's partial at amax[b * stride]
 };
 static_assert(sizeof(StepWorkspace) % 4096 == 256, "tagged vectors 256 bytes past the 4 KB grid");
 

@@ -1640,10 +1640,9 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
         if (threadIdx.x == 0) {
             KArgs &a = kargs();
             for (int k = 1; k < WAVES; k++) amax_pair(best, bidx, red_v[k], red_i[k]);
-            __hip_atomic_store(gptr((unsigned *)&a.amax_val[blockIdx.x]), __float_as_uint(best),
+            __hip_atomic_store(gptr(a.amax + AMAX_STRIDE * blockIdx.x),
+                               ((unsigned long long)__float_as_uint(best) << 32) | (unsigned)bidx,
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(gptr(&a.amax_idx[blockIdx.x]), bidx, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
             __builtin_amdgcn_s_waitcnt(0);
             // the counter runs over the launch's tokens: step s ends at (s + 1) * grid arrivals
             const unsigned done = __hip_atomic_fetch_add(gptr(a.final_ctr), 1u, __ATOMIC_RELAXED,
@@ -1665,11 +1664,10 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
                     const int k = k0 + lane + 64 * j, kk = k < (int)gridDim.x ? k : 0;
-                    pv[j] = __uint_as_float(__hip_atomic_load(gptr((unsigned *)&a.amax_val[kk]),
-                                                              __ATOMIC_RELAXED,
-                                                              __HIP_MEMORY_SCOPE_AGENT));
-                    pi[j] = __hip_atomic_load(gptr(&a.amax_idx[kk]), __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT);
+                    const unsigned long long p = __hip_atomic_load(
+                        gptr(a.amax + AMAX_STRIDE * kk), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    pv[j] = __uint_as_float((uint32_t)(p >> 32));
+                    pi[j] = (int)(uint32_t)p;
                 }
 #pragma unroll
                 for (int j = 0; j < 4; j++)
