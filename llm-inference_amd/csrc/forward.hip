@@ -333,7 +333,6 @@ static StepArgs step_args(const Config *cfg, const Weights *w, RunState *s, int 
     a.n_tokens = 1;
     step_split_buffers(cfg, s->max_seq, s->step_ws, &a.tstat, &a.tpart);
     a.max_blocks = step_split_max_blocks(cfg, s->max_seq);
-    a.final_ctr = &ws->final_ctr;
     a.amax = ws->amax;
     a.eps = cfg->rms_norm_eps;
     a.scale = (float)(1.0 / sqrt((double)cfg->head_dim));

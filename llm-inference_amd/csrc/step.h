@@ -30,10 +30,9 @@ struct StepArgs {
     uint32_t *tx, *tqkv, *tattn, *thb;
     int *next_token, *pos, *token_out, *pos_base, *error_flag;
     unsigned *epoch;      // tagged phases written over all launches (the tag base)
-    unsigned *final_ctr;  // workgroups done with the LM head (counts over a launch's tokens)
     // the next token, tagged ((token << 32) | tag), in TOKEN_COPIES copies 64 words apart
     unsigned long long *token_word;
-    // per-workgroup argmax partials, (float bits << 32) | index, AMAX_STRIDE words apart
+    // per-workgroup argmax partials, tagged 64-bit words AMAX_STRIDE words apart
     unsigned long long *amax;
     long long *trace;     // optional wall-clock stamps of one workgroup's phases
     float eps, scale;
@@ -47,8 +46,8 @@ struct StepArgs {
 };
 
 // The next token reaches every workgroup as a tagged word in up to TOKEN_COPIES copies 512 bytes
-// apart, away from the cache line of final_ctr, which every workgroup adds to once per token (a
-// shape that uses R copies has workgroup b poll copy b % R).
+// apart, each on a cache line of its own (a shape that uses R copies has workgroup b poll copy
+// b % R).
 constexpr int TOKEN_COPIES = 8;
 // Each workgroup's argmax partial (one 64-bit word) sits on a 128-byte line of its own, so the
 // workgroups' stores at the end of a token do not meet on shared lines.
@@ -59,8 +58,7 @@ constexpr int AMAX_STRIDE = 16;
 // multiple of 4 KB, which places the tagged vectors' copies 1 KB off the 4 KB grid.
 struct StepWorkspace {
     unsigned epoch;
-    unsigned final_ctr;
-    unsigned pad[62];
+    unsigned pad[63];
     unsigned long long token_word[TOKEN_COPIES][64];  // copy c at token_word[c][0]
     unsigned long long amax[1024 * AMAX_STRIDE];      // workgroup b's partial at amax[b * stride]
 };

@@ -7,8 +7,9 @@
 //   per layer:  rmsnorm + q/k/v rows | QK-norm + RoPE + KV write + attention, one workgroup
 //               per query head | o rows + residual | rmsnorm + gate/up rows + SwiGLU |
 //               down rows + residual
-//   final:      rmsnorm + LM-head rows + per-workgroup argmax; the last workgroup to finish
-//               reduces the argmax, records the token and advances the position
+//   final:      rmsnorm + LM-head rows + per-workgroup argmax, published as tagged words;
+//               one workgroup polls them, reduces the argmax, records the token, advances the
+//               position and publishes the token to the others
 //
 // Activations cross workgroups (and XCDs, whose L2s are not coherent) as tagged vectors:
 // element i is the 32-bit word (bf16 bits << 16) | tag, stored and loaded with agent-scope
@@ -1225,6 +1226,17 @@ __device__ __forceinline__ void split_attention(KArgs &a, KLayer &L, int pos, in
     }
 }
 
+// ---------------------------------------------------------------- argmax partials
+
+// A workgroup's argmax partial as one tagged 64-bit word: the value's bits << 32, the row index
+// << 14 (18 bits; AMAX_NO_ROW for a workgroup without rows, which loses every tie as INT_MAX
+// does), and the token's 14-bit tag (never 0, so a zeroed word never matches).
+constexpr int AMAX_NO_ROW = 0x3ffff;
+__device__ __forceinline__ unsigned long long amax_word(float v, int i, uint32_t tag) {
+    const uint32_t ix = i >= 0 && i < AMAX_NO_ROW ? (uint32_t)i : (uint32_t)AMAX_NO_ROW;
+    return ((unsigned long long)__float_as_uint(v) << 32) | (ix << 14) | tag;
+}
+
 // ---------------------------------------------------------------- the step
 
 // Rows [r0, r1) of a phase with R rows owned by wave w of this workgroup, the rows spread in
@@ -1294,7 +1306,6 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
     } sm;
     __shared__ float red_v[WAVES];
     __shared__ int red_i[WAVES];
-    __shared__ int last_wg;
     __shared__ uint32_t out_stage[WAVES * 64];  // a workgroup's x rows as tagged words
     __shared__ float norm_inv;
 
@@ -1637,43 +1648,51 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
             red_i[w] = bidx;
         }
         __syncthreads();
+        // this token's tag for the argmax partials (1..16383, 14 bits; consecutive tokens differ)
+        const uint32_t ptag = 1u + tag_of(seq_end) % 16383u;
         if (threadIdx.x == 0) {
             KArgs &a = kargs();
             for (int k = 1; k < WAVES; k++) amax_pair(best, bidx, red_v[k], red_i[k]);
-            __hip_atomic_store(gptr(a.amax + AMAX_STRIDE * blockIdx.x),
-                               ((unsigned long long)__float_as_uint(best) << 32) | (unsigned)bidx,
+            __hip_atomic_store(gptr(a.amax + AMAX_STRIDE * blockIdx.x), amax_word(best, bidx, ptag),
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __builtin_amdgcn_s_waitcnt(0);
-            // the counter runs over the launch's tokens: step s ends at (s + 1) * grid arrivals
-            const unsigned done = __hip_atomic_fetch_add(gptr(a.final_ctr), 1u, __ATOMIC_RELAXED,
-                                                         __HIP_MEMORY_SCOPE_AGENT);
-            last_wg = done == (unsigned)(step + 1) * gridDim.x - 1;
         }
-        __syncthreads();
-        if (last_wg && w == 0) {
-            // the last workgroup: every partial is complete; the wave reduces them in parallel
+        // the workgroup that reduces the partials and publishes the token
+        const int reducer = S::ARGMAX_FIRST_WG ? 0 : (int)gridDim.x - 1;
+        int chosen = 0;  // the reducer's wave 0: this step's token
+        if ((int)blockIdx.x == reducer && w == 0) {
+            // the reducer polls every workgroup's partial (its own included) until each carries
+            // this token's tag, then reduces them in the order k = lane, lane + 64, ...; every
+            // partial of a round of 256 is requested before any is compared, and a lane past
+            // the grid reads partial 0 and ignores it
             KArgs &a = kargs();
             float v = -__builtin_huge_valf();
             int idx = INT_MAX;
-            // every partial of a round of 256 requested before any is compared (one loop step per
-            // 64 partials would wait for each step's loads in turn), then compared in the order
-            // k = lane, lane + 64, ...; a lane past the grid reads partial 0 and ignores it
             for (int k0 = 0; k0 < (int)gridDim.x; k0 += 4 * 64) {
-                float pv[4];
-                int pi[4];
+                unsigned long long p[4];
+                long long spins = 0;
+                for (;;) {
+                    bool fresh = true;
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const int k = k0 + lane + 64 * j, kk = k < (int)gridDim.x ? k : 0;
-                    const unsigned long long p = __hip_atomic_load(
-                        gptr(a.amax + AMAX_STRIDE * kk), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    pv[j] = __uint_as_float((uint32_t)(p >> 32));
-                    pi[j] = (int)(uint32_t)p;
+                    for (int j = 0; j < 4; j++) {
+                        const int k = k0 + lane + 64 * j, kk = k < (int)gridDim.x ? k : 0;
+                        p[j] = __hip_atomic_load(gptr(a.amax + AMAX_STRIDE * kk), __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+                        fresh &= (uint32_t)(p[j] & 0x3fffu) == ptag;
+                    }
+                    if (fresh) break;
+                    if ((++spins & 63) == 0 && wait_gives_up(spins, SPIN_LIMIT, a.error_flag))
+                        break;
                 }
 #pragma unroll
-                for (int j = 0; j < 4; j++)
-                    if (k0 + lane + 64 * j < (int)gridDim.x) amax_pair(v, idx, pv[j], pi[j]);
+                for (int j = 0; j < 4; j++) {
+                    const int i = (int)((p[j] >> 14) & AMAX_NO_ROW);
+                    if (k0 + lane + 64 * j < (int)gridDim.x)
+                        amax_pair(v, idx, __uint_as_float((uint32_t)(p[j] >> 32)),
+                                  i == AMAX_NO_ROW ? INT_MAX : i);
+                }
             }
             wave_amax(v, idx);
+            chosen = idx;
             if (step + 1 < n_tokens && lane < S::TOKEN_COPIES) {
                 // the next token for every workgroup, one copy per lane
                 __hip_atomic_store(gptr(a.token_word + 64 * lane),
@@ -1688,7 +1707,6 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                     *gptr(a.pos) = pos + 1;
                 }
                 if (step + 1 >= n_tokens) {
-                    *gptr(a.final_ctr) = 0;
                     *gptr(a.epoch) = seq0 + n_tokens * seq_step;
                     if (a.trace) gptr(a.trace)[2 + 4 * n_layers] = wall_clock64();
                 }
@@ -1697,7 +1715,9 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
         if (step + 1 < n_tokens) {
             // wait for the token this step chose (bounded like every other wait)
             __shared__ int next_tok;
-            if (threadIdx.x == 0) {
+            if (threadIdx.x == 0 && (int)blockIdx.x == reducer) {
+                next_tok = chosen;  // the workgroup that chose it
+            } else if (threadIdx.x == 0) {
                 KArgs &a = kargs();
                 unsigned long long tw = 0;
                 long long spins = 0;
@@ -1805,6 +1825,12 @@ struct Shape {
     // word shared the cache line of the counter every workgroup adds to once per token
     // (alternating runs on one box); 4B 596.8 with 8 against 594.7 with one
     static constexpr int TOKEN_COPIES = H <= 1024 ? 1 : 8;
+    // which workgroup reduces the argmax partials: the first (an attention workgroup) at 4B,
+    // 615.2-616.0 tokens/s against 598.9-599.7 for the last one and for a counter of the
+    // workgroups done (the last to arrive reducing); the last at 0.6B and 1.7B (0.6B 2472.1,
+    // first 2470.0, counter 2473.2; 1.7B 1143.3, first 1136.9, counter 1139.7; alternating
+    // runs on one box)
+    static constexpr bool ARGMAX_FIRST_WG = H > 2048;
     // 1.7B: the down rows with attention 1050 -> 1075 tokens/s, the q/k/v rows too 1005; 4B
     // (5-token prompt): 575.8-576.4 as below, the q/k/v rows after the gate/up poll 572.6-572.8,
     // the down rows after the o poll 466.2-466.3
@@ -1899,7 +1925,8 @@ void step_split_buffers(const Config *c, int max_seq, void *ws, unsigned long lo
 }
 
 bool step_kernel_available(const Config *cfg) {
-    return step_kernel_for(cfg) != nullptr && cfg->vocab_size > 0 &&
+    // (the argmax partials carry a row index in 18 bits)
+    return step_kernel_for(cfg) != nullptr && cfg->vocab_size > 0 && cfg->vocab_size < 0x3ffff &&
            step_grid_fits(cfg, step_kernel_grid());
 }
 
