@@ -329,7 +329,7 @@ static StepArgs step_args(const Config *cfg, const Weights *w, RunState *s, int 
     a.tattn = a.tqkv + step_replica_stride(qd + 2 * kvd);
     a.thb = a.tattn + STEP_REPLICAS * step_replica_stride(qd);
     a.epoch = &ws->epoch;
-    a.token_word = &ws->token_word[0][0];
+    a.token_word = &ws->token_word[0];
     a.n_tokens = 1;
     step_split_buffers(cfg, s->max_seq, s->step_ws, &a.tstat, &a.tpart);
     a.max_blocks = step_split_max_blocks(cfg, s->max_seq);

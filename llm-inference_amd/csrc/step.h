@@ -30,8 +30,7 @@ struct StepArgs {
     uint32_t *tx, *tqkv, *tattn, *thb;
     int *next_token, *pos, *token_out, *pos_base, *error_flag;
     unsigned *epoch;      // tagged phases written over all launches (the tag base)
-    // the next token, tagged ((token << 32) | tag), in TOKEN_COPIES copies 64 words apart
-    unsigned long long *token_word;
+    unsigned long long *token_word;  // the next token, tagged: (token << 32) | tag
     // per-workgroup argmax partials, tagged 64-bit words AMAX_STRIDE words apart
     unsigned long long *amax;
     long long *trace;     // optional wall-clock stamps of one workgroup's phases
@@ -45,10 +44,6 @@ struct StepArgs {
     float inv_freq[64];
 };
 
-// The next token reaches every workgroup as a tagged word in up to TOKEN_COPIES copies 512 bytes
-// apart, each on a cache line of its own (a shape that uses R copies has workgroup b poll copy
-// b % R).
-constexpr int TOKEN_COPIES = 8;
 // Each workgroup's argmax partial (one 64-bit word) sits on a 128-byte line of its own, so the
 // workgroups' stores at the end of a token do not meet on shared lines.
 constexpr int AMAX_STRIDE = 16;
@@ -59,7 +54,10 @@ constexpr int AMAX_STRIDE = 16;
 struct StepWorkspace {
     unsigned epoch;
     unsigned pad[63];
-    unsigned long long token_word[TOKEN_COPIES][64];  // copy c at token_word[c][0]
+    // the next token's word at token_word[0], alone on its cache line (every workgroup polls
+    // it; sharing the line of a word every workgroup writes once per token cost the 0.6B decode
+    // up to 2.8%); the rest of the 4 KB block is padding
+    unsigned long long token_word[512];
     unsigned long long amax[1024 * AMAX_STRIDE];      // workgroup b's partial at amax[b * stride]
 };
 static_assert(sizeof(StepWorkspace) % 4096 == 256, "tagged vectors 256 bytes past the 4 KB grid");

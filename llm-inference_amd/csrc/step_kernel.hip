@@ -1693,13 +1693,13 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
             }
             wave_amax(v, idx);
             chosen = idx;
-            if (step + 1 < n_tokens && lane < S::TOKEN_COPIES) {
-                // the next token for every workgroup, one copy per lane
-                __hip_atomic_store(gptr(a.token_word + 64 * lane),
-                                   ((unsigned long long)(unsigned)idx << 32) | tag_of(seq_end),
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
             if (lane == 0) {
+                if (step + 1 < n_tokens) {
+                    // the next token for every workgroup
+                    __hip_atomic_store(gptr(a.token_word),
+                                       ((unsigned long long)(unsigned)idx << 32) | tag_of(seq_end),
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
                 *gptr(a.next_token) = idx;
                 if (a.advance) {
                     const int i = pos - *gptr(a.pos_base);
@@ -1722,9 +1722,8 @@ __global__ __launch_bounds__(THREADS) void step_kernel(StepArgs) {
                 unsigned long long tw = 0;
                 long long spins = 0;
                 for (;;) {
-                    tw = __hip_atomic_load(
-                        gptr(a.token_word + 64 * ((int)blockIdx.x % S::TOKEN_COPIES)),
-                        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    tw = __hip_atomic_load(gptr(a.token_word), __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
                     if ((uint32_t)tw == tag_of(seq_end)) break;
                     if ((++spins & 63) == 0 && wait_gives_up(spins, SPIN_LIMIT, a.error_flag))
                         break;
@@ -1820,11 +1819,6 @@ struct Shape {
     // 2 copies 2258); before that layout 4 measured faster (2291-2294 against 2280-2282 with 8,
     // 2301 against 2221 with 2 and 2067 with 3). 1.7B and 4B: 4 (1.7B 1115 against 1074 with 8).
     static constexpr int REPLICAS = H == 1024 ? 8 : 4;
-    // copies of the next token's word the workgroups poll (at most TOKEN_COPIES), each on a
-    // cache line of its own: 0.6B 2486.4 tokens/s with one, 2478.3 with 8, 2417.6 when the one
-    // word shared the cache line of the counter every workgroup adds to once per token
-    // (alternating runs on one box); 4B 596.8 with 8 against 594.7 with one
-    static constexpr int TOKEN_COPIES = H <= 1024 ? 1 : 8;
     // which workgroup reduces the argmax partials: the first (an attention workgroup) at 4B,
     // 615.2-616.0 tokens/s against 598.9-599.7 for the last one and for a counter of the
     // workgroups done (the last to arrive reducing); the last at 0.6B and 1.7B (0.6B 2472.1,
