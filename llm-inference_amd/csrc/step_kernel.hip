@@ -134,13 +134,15 @@ __device__ __forceinline__ const uint32_t *my_copy(const uint32_t *v) {
 // wave that has none. Otherwise every thread polls (p = threadIdx.x + THREADS j). The workgroup
 // syncs before (the previous contents of dst have been read) and after. Bounded: once the error
 // flag is set (an earlier error, or another wait that timed out), or when its own polls run out
-// (the flag then becomes 2 unless already set), it goes on with what it read.
-template <int PAIRS, bool ONE_WAVE, class Src>
+// (the flag then becomes 2 unless already set), it goes on with what it read. With IDLE_OUT,
+// waves wholly past the pairs (a wave-uniform test) stay out of the poll instead of re-reading
+// the last pair.
+template <int PAIRS, bool ONE_WAVE, bool IDLE_OUT = false, class Src>
 __device__ __forceinline__ void stage_pairs(Src src, uint32_t tag, uint32_t *dst, int *err) {
     constexpr int STEP = ONE_WAVE ? 64 : THREADS;
     constexpr int P = (PAIRS + STEP - 1) / STEP;
     __syncthreads();
-    if (!ONE_WAVE || wave_id() == 0) {
+    if (ONE_WAVE ? wave_id() == 0 : !IDLE_OUT || wave_id() * 64 < PAIRS) {
         const int t0 = ONE_WAVE ? (tid_x() & 63) : (int)threadIdx.x;
         // Every lane issues every poll (a lane past the pairs re-reads the last one), so no
         // branch surrounds a load.
@@ -561,7 +563,10 @@ __device__ __forceinline__ void attention_head(KArgs &a, KLayer &L, int h, int p
     {
         const uint32_t *qkv = a.tqkv;
         const int qo = h * D, ko = QD + g * D, vo = QD + KVD + g * D;
-        stage_pairs<3 * D / 2, false>(
+        // the waves past the 192 pairs stay out of the poll where two query heads share a kv
+        // head (0.6B 2436.8 -> 2446.0 tokens/s, 1.7B 1140.6 -> 1145.3); at 4B they poll too
+        // (612.8 against 599.6 without them)
+        stage_pairs<3 * D / 2, false, S::H <= 2048>(
             [=](int p) {
                 // segment p / 64: q, k or v (arithmetic, not a select chain, which the compiler
                 // turns into a table in scratch memory)
