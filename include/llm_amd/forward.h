@@ -157,7 +157,7 @@ enum { ATTN_AUTO = 0, ATTN_SEPARATE = 1, ATTN_IN_SCORES = 2, ATTN_ONE_PASS = 3 }
  * per query head up to 448 / 384 / 512 positions at 0.6B / 1.7B / 4B, and split over
  * (kv head, 64-position block) items on every workgroup from there on, up to the kernel's
  * longest history (12288 positions on 256 CUs: the switch; the graph leads by at most 4%,
- * between ~5000 and ~7500 positions at 1.7B and 4B). 5-token prompt: 2467 / 1145 / 614 tokens/s against
+ * between ~5000 and ~7500 positions at 1.7B and 4B). 5-token prompt: 2476 / 1145 / 615 tokens/s against
  * 1278 / 893 / 492 for the graph; 0.6B after 4096 / 8192 positions 1450 / 1274 against 1138 /
  * 1035. Other shapes: the hipGraph. STEP_GRAPH: always the hipGraph. STEP_PERSISTENT: the
  * persistent kernel at every position (max_seq at most the kernel's longest history) or an
